@@ -1,0 +1,245 @@
+#!/usr/bin/env python3
+"""Benchmark of the tree-verification hot path on one MI355X.
+
+Workload (the headline configuration): one layer of bf16 tree verification,
+Llama-3.1-8B attention shape (32 query heads, 8 KV heads, head_dim 128),
+batch 1, a 65536-token prefix in 16-token pages behind a random-permutation
+page table, a 64-node draft tree (parents from the seeded generator, depth
+<= 8, out-degree <= 4) whose K/V follow the prefix in the same pages.  One
+step = the fused verify: kernel 1 (split-K flash-decoding over the pages plus
+the ancestor-masked tree split) and kernel 3 (LSE merge) -> O [64, 32, 128]
+bf16 + LSE [64, 32].  Four distinct KV layers are rotated so the 256 MiB
+per-layer K/V set is not served from the 256 MB Infinity Cache.
+
+Also measured (extra fields): the acceptance kernel on 8 trees x 64 nodes x
+vocab 128256 bf16 (greedy and typical), and the CPU baseline — the
+reference's own torch CPU path (repeat_kv -> fp32 matmul/softmax/logsumexp
+prefix -> naive tree -> sigmoid merge) on the same workload, timed on the
+host cores.
+
+Prints ONE JSON line.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "specdiff-ae_amd"))
+sys.path.insert(0, str(REPO))
+
+import torch  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, AMD public spec
+
+
+def algorithmic_bytes(n_prefix, M, H, Hk, D, elem=2, out_elem=2, page_size=16):
+    kv = 2 * n_prefix * Hk * D * elem
+    q = M * H * D * elem
+    tree_kv = 2 * M * Hk * D * elem
+    o = M * H * D * out_elem
+    lse = 4 * M * H
+    pt = 4 * ((n_prefix + M + page_size - 1) // page_size)
+    return {"step": kv + q + tree_kv + o + lse + pt, "kernel1": kv + q + tree_kv + pt, "prefix_kv": kv}
+
+
+class HipEvents:
+    """hipEvent_t pairs from the HIP runtime torch loaded (same soname)."""
+
+    def __init__(self):
+        self.hip = ctypes.CDLL("libamdhip64.so.7")
+        self.hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+
+    def create(self, n):
+        evs = []
+        for _ in range(n):
+            e = ctypes.c_void_p()
+            rc = self.hip.hipEventCreate(ctypes.byref(e))
+            if rc != 0:
+                raise RuntimeError(f"hipEventCreate failed ({rc})")
+            evs.append(e)
+        return evs
+
+    def elapsed_ms(self, a, b):
+        ms = ctypes.c_float()
+        rc = self.hip.hipEventElapsedTime(ctypes.byref(ms), a, b)
+        if rc != 0:
+            raise RuntimeError(f"hipEventElapsedTime failed ({rc})")
+        return ms.value
+
+    def destroy(self, evs):
+        for e in evs:
+            self.hip.hipEventDestroy(e)
+
+
+def bench_verify(args, lib, ev):
+    from diffspec_mi355x import workloads as wl
+    from diffspec_mi355x.runtime.tree_attention import tree_verify
+
+    n_prefix, M, H, Hk, D = args.n_prefix, args.nodes, 32, 8, 128
+    inp = wl.make_tree_verify_inputs(n_prefix=n_prefix, M=M, H=H, Hk=Hk, D=D, layers=args.layers,
+                                     device="cuda", seed=0, tree_seed=0)
+    par = torch.tensor(inp.parent, dtype=torch.int64, device="cuda")
+    pools = [(inp.kv_pages[l, 0], inp.kv_pages[l, 1]) for l in range(args.layers)]
+
+    def step(i, arm=None):
+        if arm is not None:
+            lib.dsv_set_timing_events(arm[0], arm[1])
+        k, v = pools[i % len(pools)]
+        return tree_verify(inp.q, k, v, n_prefix, par, page_table=inp.page_table)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    # Timed region: K whole steps (kernel 1 + kernel 3), device clock.
+    k1 = ev.create(2 * args.steps)
+    st0, st1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter()
+    st0.record()
+    for i in range(args.steps):
+        step(i, arm=(k1[2 * i], k1[2 * i + 1]))
+    st1.record()
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter() - t_wall
+    total_ms = st0.elapsed_time(st1)
+    k1_ms = [ev.elapsed_ms(k1[2 * i], k1[2 * i + 1]) for i in range(args.steps)]
+    ev.destroy(k1)
+    return inp, total_ms / args.steps, k1_ms, t_wall
+
+
+def bench_accept(args, lib, ev):
+    from diffspec_mi355x import workloads as wl
+    from diffspec_mi355x.draft.tree_verification import tree_accept
+
+    T, M, V = 8, 64, 128256
+    a = wl.make_accept_inputs(T=T, M=M, V=V, device="cuda", pos_offset=65536)
+    res = {}
+    for mode in ("greedy", "typical"):
+        for _ in range(3):
+            tree_accept(a.logits, a.draft, a.parent_ref, a.pos, 10, mode=mode)
+        torch.cuda.synchronize()
+        n = 20
+        evs = ev.create(2 * n)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(n):
+            lib.dsv_set_timing_events(evs[2 * i], evs[2 * i + 1])
+            r = tree_accept(a.logits, a.draft, a.parent_ref, a.pos, 10, mode=mode)
+        e1.record()
+        torch.cuda.synchronize()
+        sweep = statistics.median(ev.elapsed_ms(evs[2 * i], evs[2 * i + 1]) for i in range(n))
+        ev.destroy(evs)
+        res[mode] = {"us_total": e0.elapsed_time(e1) / n * 1e3, "us_vocab_sweep": sweep * 1e3,
+                     "accept_lengths": r["info"][:, 1].tolist()}
+    nbytes = T * M * V * 2
+    for mode in res:
+        res[mode]["sweep_gbs"] = nbytes / (res[mode]["us_vocab_sweep"] * 1e-6) / 1e9
+    return res
+
+
+def cpu_baseline(inp, args):
+    """Reference CPU path (oracle/ref_cpu_path.py) on the same layer, bounded sample."""
+    from oracle import ref_cpu_path as rc
+    from oracle import attention as oa
+
+    cores = len(os.sched_getaffinity(0))
+    cores = min(cores, int(os.environ.get("BENCH_CPU_THREADS", "16")))
+    torch.set_num_threads(cores)
+    n_prefix, M = inp.n_prefix, inp.M
+    k = inp.logical_kv(0, 0)[0].float().cpu().transpose(0, 1).unsqueeze(0).contiguous()  # [1, Hk, L, D]
+    v = inp.logical_kv(0, 1)[0].float().cpu().transpose(0, 1).unsqueeze(0).contiguous()
+    q = inp.q.float().cpu()
+    mask = rc.additive_tree_mask(torch.from_numpy(oa.ancestor_mask(inp.parent)))
+    times = []
+    t_end = time.perf_counter() + args.cpu_seconds
+    while time.perf_counter() < t_end or not times:
+        t0 = time.perf_counter()
+        out = rc.hybrid_verify_cpu(q, k, v, n_prefix, mask)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= args.cpu_max_steps:
+            break
+    return {"value": statistics.median(times) * 1e6, "unit": "us/verify-step", "cores": cores, "kind": "port",
+            "sample": f"{len(times)} full config-2 verify steps (1 layer, N={n_prefix}, M={M}, fp32 upcast), "
+                      f"median"}, out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--n-prefix", type=int, default=65536)
+    ap.add_argument("--nodes", type=int, default=64)
+    ap.add_argument("--layers", type=int, default=4)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-max-steps", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-accept", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (got --gpus {args.gpus}). "
+              "Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(1)
+
+    from diffspec_mi355x import _ext
+
+    lib = _ext.load()
+    ev = HipEvents()
+    print(f"[bench] verify: N={args.n_prefix} M={args.nodes} steps={args.steps} warmup={args.warmup}", file=sys.stderr,
+          flush=True)
+    inp, ms_step, k1_ms, t_wall = bench_verify(args, lib, ev)
+    nb = algorithmic_bytes(args.n_prefix, args.nodes, 32, 8, 128)
+    us_step = ms_step * 1e3
+    k1_us = statistics.mean(k1_ms) * 1e3
+    k1_med = statistics.median(k1_ms) * 1e3
+    achieved = nb["kernel1"] / (k1_us * 1e-6) / 1e9
+    line = {
+        "metric": "verify-step us & HBM GB/s (% peak) at 64K ctx, 64-node tree, 1 MI355X",
+        "value": round(us_step, 3),
+        "unit": "us/verify-step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1)*0.5 Q/K/V, random-permutation page table, generated tree)",
+        "config": {"workload": "tree-verify attention, 1 layer, paged bf16 KV", "n_prefix": args.n_prefix,
+                   "tree_nodes": args.nodes, "q_heads": 32, "kv_heads": 8, "head_dim": 128, "page_size": 16,
+                   "batch": 1, "kv_layers_rotated": args.layers},
+        "hbm_gbs_step": round(nb["step"] / (us_step * 1e-6) / 1e9, 1),
+        "hbm_frac_step": round(nb["step"] / (us_step * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "roofline": {"kernel": "attn_splitk_kernel (kernel 1: prefix splits + tree split)", "bound": "hbm",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": nb["kernel1"], "avg_us": round(k1_us, 3), "median_us": round(k1_med, 3)},
+        "wall_s_timed": round(t_wall, 4),
+    }
+    if not args.no_accept:
+        print("[bench] acceptance kernel", file=sys.stderr, flush=True)
+        line["acceptance"] = bench_accept(args, lib, ev)
+    if not args.no_cpu:
+        print("[bench] CPU baseline", file=sys.stderr, flush=True)
+        cb, _ = cpu_baseline(inp, args)
+        line["cpu_baseline"] = cb
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,218 @@
+/*
+ * dsv.h — C ABI of the MI355X (gfx950) tree-verification library (libdsv.so).
+ *
+ * The library implements the target-side tree-verification hot path of
+ * DiffSpec: tree-masked, grouped-query attention of a draft tree's nodes
+ * against a long (optionally paged) KV prefix, and the tree acceptance walk
+ * that follows it.  Every entry point below replaces one function of the
+ * reference's Python API; the citation names the reference file:line whose
+ * contract (argument meaning, shapes, layouts, error behaviour) it follows.
+ *
+ * Conventions
+ *   - All tensors are caller-owned device memory described by dsv_tensor
+ *     (pointer + dtype + shape + strides in elements).  No torch types cross
+ *     this boundary.  The innermost (head_dim / vocab) stride must be 1.
+ *   - Every function returns DSV_OK (0) or a negative error code; the text of
+ *     the last error on the calling thread is available from dsv_last_error().
+ *     No C++ exception crosses the ABI and there is no silent fallback.
+ *   - Work is enqueued on the caller's HIP stream; functions never synchronise
+ *     the device.  Scratch memory comes from a caller-allocated workspace whose
+ *     size the matching *_workspace_bytes() function returns.
+ *   - Functions are stateless and re-entrant; concurrent calls on different
+ *     streams must use different workspaces.
+ */
+#ifndef DSV_H_
+#define DSV_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DSV_MAX_DIMS 6
+
+typedef enum dsv_dtype {
+  DSV_BF16 = 0,
+  DSV_F16 = 1,
+  DSV_F32 = 2,
+  DSV_I8 = 3,
+  DSV_U8 = 4,
+  DSV_BOOL = 5,
+  DSV_I32 = 6,
+  DSV_I64 = 7
+} dsv_dtype;
+
+typedef enum dsv_status {
+  DSV_OK = 0,
+  DSV_ERR_INVALID = -1,     /* bad shape / dtype / stride / argument */
+  DSV_ERR_UNSUPPORTED = -2, /* valid request outside what the kernels implement */
+  DSV_ERR_WORKSPACE = -3,   /* workspace missing or too small */
+  DSV_ERR_HIP = -4          /* a HIP runtime call failed */
+} dsv_status;
+
+typedef struct dsv_tensor {
+  void* data;                      /* device pointer (may be NULL only when ndim == 0) */
+  int32_t dtype;                   /* dsv_dtype */
+  int32_t ndim;                    /* 0 means "absent" for optional arguments */
+  int64_t shape[DSV_MAX_DIMS];
+  int64_t stride[DSV_MAX_DIMS];    /* in elements */
+} dsv_tensor;
+
+/* Library identification and error text. */
+int dsv_version(void);
+const char* dsv_last_error(void);
+
+/*
+ * Instrumentation (no reference counterpart; the reference times phases with
+ * host clocks under DIFFSPEC_PROFILE, draft/diffspec_model.py:594-605).
+ * Arms a one-shot pair of caller-created hipEvent_t handles: the next entry
+ * point called on this thread records `start` on its stream right before its
+ * main kernel (kernel 1 for attention, the vocab sweep for acceptance) and
+ * `stop` right after it, then disarms.  Pass NULLs to disarm.
+ */
+int dsv_set_timing_events(void* start_event, void* stop_event);
+
+/* ------------------------------------------------------------------------- */
+/* Attention (kernels 1-3: split-K flash-decoding, tree-ancestor block, merge) */
+/* ------------------------------------------------------------------------- */
+
+/*
+ * Workspace needed by any attention entry point for queries of shape
+ * [B, M, H, D] against keys with Hk heads and n_keys prefix keys, with an
+ * optional tree block (has_tree != 0).  Returns 0 on invalid arguments.
+ */
+size_t dsv_attn_workspace_bytes(int64_t B, int64_t M, int64_t H, int64_t Hk,
+                                int64_t D, int64_t n_keys, int64_t page_size,
+                                int has_tree);
+
+/*
+ * prefix_attention_forward — runtime/tree_attention.py:414-446; LSE layout of
+ * flash_attn_with_kvcache(return_softmax_lse=True), runtime/attention_compat.py:103-132.
+ *   q   [B, M, H, D] bf16|f16
+ *   k,v [B, N, Hk, D] same dtype; H % Hk == 0 (Hk == H is the repeat_kv'd form)
+ *   n_keys  keys [0, n_keys) are attended (cache_seqlens); n_keys < 0 means N
+ *   out [B, M, H, D] q dtype or f32;  lse [B, H, M] f32 (natural log)
+ */
+int dsv_prefix_attention_forward(const dsv_tensor* q, const dsv_tensor* k,
+                                 const dsv_tensor* v, int64_t n_keys,
+                                 dsv_tensor* out, dsv_tensor* lse,
+                                 void* workspace, size_t workspace_bytes,
+                                 void* stream);
+
+/*
+ * tree_attention_forward — runtime/tree_attention.py:462-541 (mask handling of
+ * _maybe_to_int8_mask, :449-460).
+ *   q   [B, M, H, D];  k, v [B, M, Hk, D] (the post-cache tree block)
+ *   tree_mask  [B, 1, T, T] or [B, T, T] with T >= M; the lower-right M x M
+ *              block is used.  Float masks are additive (keep where == 0);
+ *              int8 / uint8 / bool masks keep where != 0.
+ *   prefix_lse [B, H, M] f32 (any layout reshaping to it, as the reference's
+ *              reshape(B, H, M, -1) does)
+ *   current_out [B, M, H, D] q dtype;  weight [B, M, H, 1] q dtype with
+ *              weight = sigmoid(prefix_lse - tree_lse)
+ *   tree_lse   optional [B, M, H] f32 output (ndim == 0 to skip)
+ */
+int dsv_tree_attention_forward(const dsv_tensor* q, const dsv_tensor* k,
+                               const dsv_tensor* v, const dsv_tensor* tree_mask,
+                               const dsv_tensor* prefix_lse,
+                               dsv_tensor* current_out, dsv_tensor* weight,
+                               dsv_tensor* tree_lse, void* workspace,
+                               size_t workspace_bytes, void* stream);
+
+/*
+ * FusedBundleVerifier.verify_bundle — runtime/bundle_verifier.py:166-297.
+ * Masked attention of q [B, M, H, D] over k, v [B, N, Hk, D] with an int8 /
+ * uint8 / bool mask [Bm, M, N] (Bm in {1, B}; 1 = keep).  shared_prefix_len
+ * does not change the result in the reference (both phases apply the mask)
+ * and is therefore not an argument.
+ *   out [B, M, H, D] q dtype or f32;  lse [B, M, H] f32
+ */
+int dsv_verify_bundle(const dsv_tensor* q, const dsv_tensor* k,
+                      const dsv_tensor* v, const dsv_tensor* mask,
+                      dsv_tensor* out, dsv_tensor* lse, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+/*
+ * PagedBundleVerifier.verify_bundle_paged — runtime/bundle_verifier.py:341-366
+ * (unimplemented in the reference; page-pool layout of
+ * core/kv_cache/paged_kv.py:56-65, page list of :325-340).
+ *   kv_pages   [L, 2, P, Hk, page_size, D]; page_size a power of two
+ *   page_table [n_pages] or [B, n_pages] int32|int64 logical -> physical page
+ *   mask       [Bm, M, N] int8|uint8|bool over the logical token sequence
+ *   out [B, M, H, D];  lse [B, M, H] f32
+ */
+int dsv_verify_bundle_paged(const dsv_tensor* q, const dsv_tensor* kv_pages,
+                            const dsv_tensor* page_table, int64_t layer_idx,
+                            const dsv_tensor* mask, dsv_tensor* out,
+                            dsv_tensor* lse, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
+/*
+ * Fused tree verification over a paged (or contiguous) KV cache: the hybrid
+ * branch of the target attention, llama_target_model.py:834-867 (prefix
+ * attention + tree-masked attention + sigmoid-LSE merge), computed in one
+ * launch of kernel 1 (S prefix splits + one tree split whose ancestor bitmask
+ * is built in-kernel from the parent array) and one launch of kernel 3.
+ *   q          [B, M, H, D]
+ *   k, v       either a page pool half kv_pages[layer, 0|1] viewed as
+ *              [P, Hk, page_size, D] together with page_table [B|-, n_pages],
+ *              or a contiguous cache [B, L, Hk, D] (page_table->ndim == 0).
+ *   n_prefix   tokens [0, n_prefix) are the prefix; the tree's K/V rows are
+ *              tokens [n_prefix, n_prefix + M) of the same cache
+ *              (KVCache.cat layout, runtime/cache_state.py:52-66)
+ *   parent     [B, M] or [M] int32|int64: parent node of each tree node, < 0 for
+ *              the root (the ancestor relation of runtime/draft_tree.py:188-214)
+ *   row_perm   optional [M] int32 node order used to pack query rows (bundle
+ *              order, core/bundle_scheduler.py:42-123); ndim == 0 = identity
+ *   out [B, M, H, D] bf16|f16|f32;  lse [B, M, H] f32 (ndim == 0 to skip)
+ */
+int dsv_tree_verify(const dsv_tensor* q, const dsv_tensor* k,
+                    const dsv_tensor* v, const dsv_tensor* page_table,
+                    int64_t n_prefix, const dsv_tensor* parent,
+                    const dsv_tensor* row_perm, dsv_tensor* out,
+                    dsv_tensor* lse, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
+/* ------------------------------------------------------------------------- */
+/* Acceptance (kernel 4)                                                      */
+/* ------------------------------------------------------------------------- */
+
+#define DSV_ACCEPT_GREEDY 0
+#define DSV_ACCEPT_TYPICAL 1
+
+/* Workspace for dsv_tree_accept with T trees of M nodes over vocab V. */
+size_t dsv_accept_workspace_bytes(int64_t T, int64_t M, int64_t V);
+
+/*
+ * Tree acceptance walk — draft/tree_verification.py:100-182 (greedy:
+ * next = argmax(logits), ok[i] = draft[i] == next[parent_ext[i]], bounded
+ * ancestor closure of max_hops rounds, winner = argmax(where(ok, pos, 0)),
+ * traceback, next token = next[winner]).  Typical mode replaces the greedy
+ * test with the posterior criterion p_T(draft[i] | parent) >
+ * min(posterior_threshold, posterior_alpha * exp(-H(p_T(. | parent)))).
+ *   logits  [T, M, V] bf16|f16|f32
+ *   draft   [T, M] int64   draft token of every node (node 0 = root)
+ *   parent  [T, M-1] int64 reference convention: parent[k] is the parent of
+ *           node k+1 among the non-root nodes; -1 or k itself = the root
+ *   pos     [T, M] or [M] int64 position ids
+ *   max_hops  closure rounds, min(max_depth + 2, M) in the reference
+ *   out_path  [T, M] int64: accepted node ids root..winner, then -1
+ *   out_tokens[T, M] int64: draft tokens along the path, then -1
+ *   out_info  [T, 4] int64: {winner node, accept_length, next_token, path_len}
+ *   out_next  optional [T, M] int64: per-node argmax token (ndim == 0 to skip)
+ */
+int dsv_tree_accept(int mode, const dsv_tensor* logits, const dsv_tensor* draft,
+                    const dsv_tensor* parent, const dsv_tensor* pos,
+                    int64_t max_hops, float temperature,
+                    float posterior_threshold, float posterior_alpha,
+                    dsv_tensor* out_path, dsv_tensor* out_tokens,
+                    dsv_tensor* out_info, dsv_tensor* out_next,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSV_H_ */

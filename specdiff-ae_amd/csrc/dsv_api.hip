@@ -1,0 +1,698 @@
+// dsv_api.hip — C ABI of libdsv.so: argument validation, split planning,
+// workspace carving and kernel launches.  Declarations and the reference
+// interface each entry point replaces are in include/dsv.h.
+
+#include "dsv.h"
+#include "dsv_internal.h"
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+namespace dsv {
+size_t accept_walk_lds_bytes(int M);
+}
+
+namespace {
+
+using dsv::AcceptArgs;
+using dsv::AttnArgs;
+using dsv::KvSrc;
+using dsv::MergeArgs;
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(DSV_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+int elem_size(int dt) {
+  switch (dt) {
+    case DSV_BF16:
+    case DSV_F16: return 2;
+    case DSV_F32:
+    case DSV_I32: return 4;
+    case DSV_I64: return 8;
+    case DSV_I8:
+    case DSV_U8:
+    case DSV_BOOL: return 1;
+    default: return 0;
+  }
+}
+
+const char* dt_name(int dt) {
+  static const char* names[] = {"bf16", "f16", "f32", "int8", "uint8", "bool", "int32", "int64"};
+  return (dt >= 0 && dt <= 7) ? names[dt] : "?";
+}
+
+bool present(const dsv_tensor* t) { return t != nullptr && t->ndim > 0; }
+
+int check_nd(const dsv_tensor* t, const char* name, int ndim) {
+  if (t == nullptr || t->ndim != ndim)
+    return fail(DSV_ERR_INVALID, "%s must be a %d-d tensor (got %d-d)", name, ndim, t ? t->ndim : -1);
+  if (t->data == nullptr) return fail(DSV_ERR_INVALID, "%s has a null data pointer", name);
+  if (elem_size(t->dtype) == 0) return fail(DSV_ERR_INVALID, "%s has an unknown dtype %d", name, t->dtype);
+  for (int i = 0; i < ndim; ++i)
+    if (t->shape[i] < 0) return fail(DSV_ERR_INVALID, "%s has a negative extent", name);
+  return DSV_OK;
+}
+
+// 16-bit operand read with 16-byte vector loads: innermost stride 1, other
+// strides multiples of 8 elements, 16-byte aligned base.
+int check_vec16(const dsv_tensor* t, const char* name, int skip_dim = -1) {
+  if (t->dtype != DSV_BF16 && t->dtype != DSV_F16)
+    return fail(DSV_ERR_UNSUPPORTED, "%s: dtype %s is not supported by the MI355X kernels (bf16 or f16 required)",
+                name, dt_name(t->dtype));
+  if (t->stride[t->ndim - 1] != 1) return fail(DSV_ERR_INVALID, "%s: innermost stride must be 1", name);
+  if ((reinterpret_cast<uintptr_t>(t->data) & 15) != 0)
+    return fail(DSV_ERR_INVALID, "%s: data pointer must be 16-byte aligned", name);
+  for (int i = 0; i < t->ndim - 1; ++i) {
+    if (i == skip_dim) continue;
+    if (t->shape[i] > 1 && (t->stride[i] % 8) != 0)
+      return fail(DSV_ERR_INVALID, "%s: stride[%d]=%lld is not a multiple of 8 elements", name, i,
+                  (long long)t->stride[i]);
+  }
+  return DSV_OK;
+}
+
+int device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
+struct Plan {
+  int G = 0, R = 0, n_rb = 0, n_splits = 0, s_total = 0;
+  int64_t kps = 0;
+  size_t opart_bytes = 0, ml_bytes = 0, total = 0;
+};
+
+constexpr int kRowsPerBlock = 256;
+
+size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+Plan make_plan(int64_t B, int64_t M, int64_t H, int64_t Hk, int64_t D, int64_t n_keys, int64_t page_size,
+               bool has_tree) {
+  Plan p;
+  p.G = (int)(H / Hk);
+  p.R = (int)(p.G * M);
+  p.n_rb = (int)((p.R + kRowsPerBlock - 1) / kRowsPerBlock);
+  const int64_t units = B * Hk * p.n_rb;
+  if (n_keys > 0) {
+    const int64_t cus = device_cus();
+    const int64_t avail = std::max<int64_t>(cus - (has_tree ? units : 0), units);
+    const int64_t s0 = std::max<int64_t>(1, avail / units);
+    int64_t kps_max = 16384;
+    if (page_size > 0) kps_max = std::min<int64_t>(kps_max, (int64_t)(dsv::kPageLds - 2) * page_size);
+    kps_max = std::max<int64_t>(64, kps_max / 64 * 64);
+    int64_t kps = ((n_keys + s0 - 1) / s0 + 63) / 64 * 64;
+    kps = std::min(std::max<int64_t>(kps, 64), kps_max);
+    p.kps = kps;
+    p.n_splits = (int)((n_keys + kps - 1) / kps);
+  }
+  p.s_total = p.n_splits + (has_tree ? 1 : 0);
+  const size_t rows = (size_t)p.s_total * B * Hk * p.R;
+  p.opart_bytes = align_up(rows * D * sizeof(float), 256);
+  p.ml_bytes = align_up(rows * sizeof(float2), 256);
+  p.total = p.opart_bytes + p.ml_bytes;
+  return p;
+}
+
+int log2_exact(int64_t x) {
+  if (x <= 0 || (x & (x - 1)) != 0) return -1;
+  int s = 0;
+  while ((1ll << s) < x) ++s;
+  return s;
+}
+
+// Common checks of q [B, M, H, D] and the output [B, M, H, D].
+int check_q_out(const dsv_tensor* q, const dsv_tensor* out) {
+  int rc;
+  if ((rc = check_nd(q, "q", 4)) != DSV_OK) return rc;
+  if ((rc = check_vec16(q, "q")) != DSV_OK) return rc;
+  if ((rc = check_nd(out, "out", 4)) != DSV_OK) return rc;
+  for (int i = 0; i < 4; ++i)
+    if (out->shape[i] != q->shape[i]) return fail(DSV_ERR_INVALID, "out shape must equal q shape");
+  if (out->dtype != DSV_BF16 && out->dtype != DSV_F16 && out->dtype != DSV_F32)
+    return fail(DSV_ERR_INVALID, "out dtype must be bf16, f16 or f32");
+  if (out->stride[3] != 1) return fail(DSV_ERR_INVALID, "out innermost stride must be 1");
+  const int64_t D = q->shape[3];
+  if (D != 64 && D != 128) return fail(DSV_ERR_UNSUPPORTED, "head_dim %lld is not supported (64 or 128)", (long long)D);
+  return DSV_OK;
+}
+
+int check_kv_dense(const dsv_tensor* k, const dsv_tensor* v, const dsv_tensor* q, const char* kn, const char* vn) {
+  int rc;
+  if ((rc = check_nd(k, kn, 4)) != DSV_OK) return rc;
+  if ((rc = check_nd(v, vn, 4)) != DSV_OK) return rc;
+  if ((rc = check_vec16(k, kn)) != DSV_OK) return rc;
+  if ((rc = check_vec16(v, vn)) != DSV_OK) return rc;
+  for (int i = 0; i < 4; ++i)
+    if (k->shape[i] != v->shape[i]) return fail(DSV_ERR_INVALID, "%s and %s shapes differ", kn, vn);
+  if (k->dtype != q->dtype || v->dtype != q->dtype)
+    return fail(DSV_ERR_INVALID, "q, %s and %s must share a dtype", kn, vn);
+  if (k->shape[0] != q->shape[0]) return fail(DSV_ERR_INVALID, "%s batch differs from q", kn);
+  if (k->shape[3] != q->shape[3]) return fail(DSV_ERR_INVALID, "%s head_dim differs from q", kn);
+  const int64_t H = q->shape[2], Hk = k->shape[2];
+  if (Hk <= 0 || H % Hk != 0)
+    return fail(DSV_ERR_INVALID, "query heads (%lld) must be a multiple of key heads (%lld)", (long long)H,
+                (long long)Hk);
+  return DSV_OK;
+}
+
+KvSrc dense_src(const dsv_tensor* k, const dsv_tensor* v, int64_t key0) {
+  KvSrc s{};
+  s.k = static_cast<const uint16_t*>(k->data);
+  s.v = static_cast<const uint16_t*>(v->data);
+  s.k_sb = k->shape[0] > 1 ? k->stride[0] : 0;
+  s.k_st = k->stride[1];
+  s.k_sh = k->stride[2];
+  s.v_sb = v->shape[0] > 1 ? v->stride[0] : 0;
+  s.v_st = v->stride[1];
+  s.v_sh = v->stride[2];
+  s.pt = nullptr;
+  s.key0 = key0;
+  return s;
+}
+
+int check_ws(const Plan& p, void* ws, size_t ws_bytes) {
+  if (p.total == 0) return DSV_OK;
+  if (ws == nullptr || ws_bytes < p.total)
+    return fail(DSV_ERR_WORKSPACE, "workspace of %zu bytes required (got %zu)", p.total, ws_bytes);
+  if ((reinterpret_cast<uintptr_t>(ws) & 255) != 0) return fail(DSV_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  return DSV_OK;
+}
+
+void fill_common(AttnArgs& a, const dsv_tensor* q, int64_t Hk, const Plan& p, void* ws) {
+  a.q = static_cast<const uint16_t*>(q->data);
+  a.q_sb = q->stride[0];
+  a.q_sm = q->stride[1];
+  a.q_sh = q->stride[2];
+  a.B = (int)q->shape[0];
+  a.M = (int)q->shape[1];
+  a.H = (int)q->shape[2];
+  a.Hk = (int)Hk;
+  a.G = p.G;
+  a.R = p.R;
+  a.n_rb = p.n_rb;
+  a.scale_log2 = (float)(1.4426950408889634 / sqrt((double)q->shape[3]));
+  a.n_splits = p.n_splits;
+  a.kps = p.kps;
+  a.s_total = p.s_total;
+  a.opart = static_cast<float*>(ws);
+  a.ml = reinterpret_cast<float2*>(static_cast<char*>(ws) + p.opart_bytes);
+}
+
+void fill_merge(MergeArgs& m, const AttnArgs& a, const dsv_tensor* out, int D) {
+  m.opart = a.opart;
+  m.ml = a.ml;
+  m.s_total = a.s_total;
+  m.B = a.B;
+  m.M = a.M;
+  m.H = a.H;
+  m.Hk = a.Hk;
+  m.G = a.G;
+  m.R = a.R;
+  m.D = D;
+  m.row_perm = a.row_perm;
+  m.out = out->data;
+  m.out_dtype = out->dtype;
+  m.o_sb = out->stride[0];
+  m.o_sm = out->stride[1];
+  m.o_sh = out->stride[2];
+}
+
+// One-shot timing events armed by dsv_set_timing_events (per thread).
+thread_local hipEvent_t g_ev_start = nullptr;
+thread_local hipEvent_t g_ev_stop = nullptr;
+
+void take_events(hipEvent_t& s, hipEvent_t& e) {
+  s = g_ev_start;
+  e = g_ev_stop;
+  g_ev_start = g_ev_stop = nullptr;
+}
+
+int run(const AttnArgs& a, const MergeArgs& m, int dtype, int D, bool dmask, hipStream_t st) {
+  hipEvent_t ev0, ev1;
+  take_events(ev0, ev1);
+  if (ev0 != nullptr && hipEventRecord(ev0, st) != hipSuccess) return fail(DSV_ERR_HIP, "hipEventRecord(start) failed");
+  hipError_t e = dsv::launch_attn(a, dtype, D, dmask, st);
+  if (e != hipSuccess) return hip_fail(e, "attention kernel launch");
+  if (ev1 != nullptr && hipEventRecord(ev1, st) != hipSuccess) return fail(DSV_ERR_HIP, "hipEventRecord(stop) failed");
+  e = dsv::launch_merge(m, st);
+  if (e != hipSuccess) return hip_fail(e, "merge kernel launch");
+  return DSV_OK;
+}
+
+int check_byte_mask(const dsv_tensor* mask, int64_t B, int64_t M, const char* name) {
+  int rc;
+  if ((rc = check_nd(mask, name, 3)) != DSV_OK) return rc;
+  if (mask->dtype != DSV_I8 && mask->dtype != DSV_U8 && mask->dtype != DSV_BOOL)
+    return fail(DSV_ERR_INVALID, "%s must be int8, uint8 or bool (got %s)", name, dt_name(mask->dtype));
+  if (mask->shape[0] != 1 && mask->shape[0] != B) return fail(DSV_ERR_INVALID, "%s batch must be 1 or B", name);
+  if (mask->shape[1] != M) return fail(DSV_ERR_INVALID, "%s must have M rows", name);
+  return DSV_OK;
+}
+
+// Physical page pool view: kv_pages [L, 2, P, Hk, ps, D] -> K and V halves of one layer.
+int paged_src(const dsv_tensor* kv_pages, int64_t layer, const dsv_tensor* pt, int64_t B, KvSrc& s,
+              int64_t& page_size, int64_t& Hk, int64_t& D, int64_t& capacity) {
+  int rc;
+  if ((rc = check_nd(kv_pages, "kv_pages", 6)) != DSV_OK) return rc;
+  if ((rc = check_vec16(kv_pages, "kv_pages")) != DSV_OK) return rc;
+  if (kv_pages->shape[1] != 2) return fail(DSV_ERR_INVALID, "kv_pages dim 1 must be 2 (K, V)");
+  if (layer < 0 || layer >= kv_pages->shape[0]) return fail(DSV_ERR_INVALID, "layer_idx out of range");
+  page_size = kv_pages->shape[4];
+  const int sh = log2_exact(page_size);
+  if (sh < 0) return fail(DSV_ERR_UNSUPPORTED, "page_size %lld must be a power of two", (long long)page_size);
+  if ((rc = check_nd(pt, "page_table", pt ? pt->ndim : 1)) != DSV_OK) return rc;
+  if (pt->ndim != 1 && pt->ndim != 2) return fail(DSV_ERR_INVALID, "page_table must be 1-d or 2-d");
+  if (pt->dtype != DSV_I32 && pt->dtype != DSV_I64) return fail(DSV_ERR_INVALID, "page_table must be int32 or int64");
+  if (pt->ndim == 2 && pt->shape[0] != B && pt->shape[0] != 1)
+    return fail(DSV_ERR_INVALID, "page_table batch must be 1 or B");
+  const int64_t npt = pt->shape[pt->ndim - 1];
+  if (pt->stride[pt->ndim - 1] != 1) return fail(DSV_ERR_INVALID, "page_table innermost stride must be 1");
+  Hk = kv_pages->shape[3];
+  D = kv_pages->shape[5];
+  const char* base = static_cast<const char*>(kv_pages->data) + layer * kv_pages->stride[0] * 2;
+  s.k = reinterpret_cast<const uint16_t*>(base);
+  s.v = reinterpret_cast<const uint16_t*>(base + kv_pages->stride[1] * 2);
+  s.k_sb = s.v_sb = 0;
+  s.k_sp = s.v_sp = kv_pages->stride[2];
+  s.k_sh = s.v_sh = kv_pages->stride[3];
+  s.k_st = s.v_st = kv_pages->stride[4];
+  s.pt = pt->data;
+  s.pt_i64 = pt->dtype == DSV_I64;
+  s.ps_shift = sh;
+  s.pt_sb = (pt->ndim == 2 && pt->shape[0] > 1) ? pt->stride[0] : 0;
+  s.key0 = 0;
+  s.n_phys = kv_pages->shape[2];
+  capacity = npt * page_size;
+  (void)B;
+  return DSV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int dsv_version(void) { return 1; }
+
+const char* dsv_last_error(void) { return g_err.c_str(); }
+
+int dsv_set_timing_events(void* start_event, void* stop_event) {
+  g_ev_start = static_cast<hipEvent_t>(start_event);
+  g_ev_stop = static_cast<hipEvent_t>(stop_event);
+  return DSV_OK;
+}
+
+size_t dsv_attn_workspace_bytes(int64_t B, int64_t M, int64_t H, int64_t Hk, int64_t D, int64_t n_keys,
+                                int64_t page_size, int has_tree) {
+  if (B <= 0 || M <= 0 || H <= 0 || Hk <= 0 || D <= 0 || H % Hk != 0 || n_keys < 0) return 0;
+  return make_plan(B, M, H, Hk, D, n_keys, page_size, has_tree != 0).total;
+}
+
+int dsv_prefix_attention_forward(const dsv_tensor* q, const dsv_tensor* k, const dsv_tensor* v, int64_t n_keys,
+                                 dsv_tensor* out, dsv_tensor* lse, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+  int rc;
+  if ((rc = check_q_out(q, out)) != DSV_OK) return rc;
+  if ((rc = check_kv_dense(k, v, q, "k", "v")) != DSV_OK) return rc;
+  const int64_t B = q->shape[0], M = q->shape[1], H = q->shape[2], D = q->shape[3];
+  const int64_t N = k->shape[1], Hk = k->shape[2];
+  if (n_keys < 0) n_keys = N;
+  if (n_keys > N) return fail(DSV_ERR_INVALID, "n_keys (%lld) exceeds the key length (%lld)", (long long)n_keys, (long long)N);
+  if ((rc = check_nd(lse, "lse", 3)) != DSV_OK) return rc;
+  if (lse->dtype != DSV_F32 || lse->shape[0] != B || lse->shape[1] != H || lse->shape[2] != M)
+    return fail(DSV_ERR_INVALID, "lse must be float32 [B, H, M]");
+  const Plan p = make_plan(B, M, H, Hk, D, n_keys, 0, false);
+  if ((rc = check_ws(p, workspace, workspace_bytes)) != DSV_OK) return rc;
+
+  AttnArgs a{};
+  fill_common(a, q, Hk, p, workspace);
+  a.pre = dense_src(k, v, 0);
+  a.n_pre = n_keys;
+  MergeArgs m{};
+  fill_merge(m, a, out, (int)D);
+  m.lse = static_cast<float*>(lse->data);
+  m.l_sb = lse->stride[0];
+  m.l_sh = lse->stride[1];
+  m.l_sm = lse->stride[2];
+  return run(a, m, q->dtype, (int)D, false, static_cast<hipStream_t>(stream));
+}
+
+int dsv_tree_attention_forward(const dsv_tensor* q, const dsv_tensor* k, const dsv_tensor* v,
+                               const dsv_tensor* tree_mask, const dsv_tensor* prefix_lse, dsv_tensor* current_out,
+                               dsv_tensor* weight, dsv_tensor* tree_lse, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+  int rc;
+  if ((rc = check_q_out(q, current_out)) != DSV_OK) return rc;
+  if ((rc = check_kv_dense(k, v, q, "key_states", "value_states")) != DSV_OK) return rc;
+  const int64_t B = q->shape[0], M = q->shape[1], H = q->shape[2], D = q->shape[3], Hk = k->shape[2];
+  if (k->shape[1] != M) return fail(DSV_ERR_INVALID, "key/value must be the post-cache block of M rows");
+  if (M > dsv::kTreeMaxM) return fail(DSV_ERR_UNSUPPORTED, "tree blocks larger than %d nodes are not supported", dsv::kTreeMaxM);
+  if (tree_mask == nullptr || (tree_mask->ndim != 3 && tree_mask->ndim != 4))
+    return fail(DSV_ERR_INVALID, "tree_mask must be [B, 1, T, T] or [B, T, T]");
+  if ((rc = check_nd(tree_mask, "tree_mask", tree_mask->ndim)) != DSV_OK) return rc;
+  const int nd = tree_mask->ndim;
+  const int64_t T0 = tree_mask->shape[nd - 2], T1 = tree_mask->shape[nd - 1];
+  if (T0 < M || T1 < M) return fail(DSV_ERR_INVALID, "tree_mask is smaller than the M x M block");
+  if (tree_mask->shape[0] != B && tree_mask->shape[0] != 1) return fail(DSV_ERR_INVALID, "tree_mask batch must be 1 or B");
+  if ((rc = check_nd(prefix_lse, "prefix_lse", 3)) != DSV_OK) return rc;
+  if (prefix_lse->dtype != DSV_F32 || prefix_lse->shape[0] != B || prefix_lse->shape[1] != H || prefix_lse->shape[2] != M)
+    return fail(DSV_ERR_INVALID, "prefix_lse must be float32 viewed as [B, H, M]");
+  if ((rc = check_nd(weight, "weight", 4)) != DSV_OK) return rc;
+  if (weight->shape[0] != B || weight->shape[1] != M || weight->shape[2] != H || weight->shape[3] != 1)
+    return fail(DSV_ERR_INVALID, "weight must be [B, M, H, 1]");
+  if (weight->dtype != DSV_BF16 && weight->dtype != DSV_F16 && weight->dtype != DSV_F32)
+    return fail(DSV_ERR_INVALID, "weight dtype must be bf16, f16 or f32");
+  if (present(tree_lse)) {
+    if ((rc = check_nd(tree_lse, "tree_lse", 3)) != DSV_OK) return rc;
+    if (tree_lse->dtype != DSV_F32 || tree_lse->shape[0] != B || tree_lse->shape[1] != M || tree_lse->shape[2] != H)
+      return fail(DSV_ERR_INVALID, "tree_lse must be float32 [B, M, H]");
+  }
+  const Plan p = make_plan(B, M, H, Hk, D, 0, 0, true);
+  if ((rc = check_ws(p, workspace, workspace_bytes)) != DSV_OK) return rc;
+
+  AttnArgs a{};
+  fill_common(a, q, Hk, p, workspace);
+  a.n_pre = 0;
+  a.has_tree = 1;
+  a.tree = dense_src(k, v, 0);
+  const int64_t es = elem_size(tree_mask->dtype);
+  const int64_t sb = tree_mask->shape[0] > 1 ? tree_mask->stride[0] : 0;
+  const int64_t sm = tree_mask->stride[nd - 2], sn = tree_mask->stride[nd - 1];
+  a.tmask = static_cast<const char*>(tree_mask->data) + ((T0 - M) * sm + (T1 - M) * sn) * es;
+  a.tmask_dtype = tree_mask->dtype;
+  a.tm_sb = sb;
+  a.tm_sm = sm;
+  a.tm_sn = sn;
+  MergeArgs m{};
+  fill_merge(m, a, current_out, (int)D);
+  if (present(tree_lse)) {
+    m.lse = static_cast<float*>(tree_lse->data);
+    m.l_sb = tree_lse->stride[0];
+    m.l_sm = tree_lse->stride[1];
+    m.l_sh = tree_lse->stride[2];
+  }
+  m.plse = static_cast<const float*>(prefix_lse->data);
+  m.p_sb = prefix_lse->stride[0];
+  m.p_sh = prefix_lse->stride[1];
+  m.p_sm = prefix_lse->stride[2];
+  m.weight = weight->data;
+  m.w_dtype = weight->dtype;
+  m.w_sb = weight->stride[0];
+  m.w_sm = weight->stride[1];
+  m.w_sh = weight->stride[2];
+  return run(a, m, q->dtype, (int)D, false, static_cast<hipStream_t>(stream));
+}
+
+int dsv_verify_bundle(const dsv_tensor* q, const dsv_tensor* k, const dsv_tensor* v, const dsv_tensor* mask,
+                      dsv_tensor* out, dsv_tensor* lse, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc;
+  if ((rc = check_q_out(q, out)) != DSV_OK) return rc;
+  if ((rc = check_kv_dense(k, v, q, "k", "v")) != DSV_OK) return rc;
+  const int64_t B = q->shape[0], M = q->shape[1], H = q->shape[2], D = q->shape[3];
+  const int64_t N = k->shape[1], Hk = k->shape[2];
+  if ((rc = check_byte_mask(mask, B, M, "mask")) != DSV_OK) return rc;
+  if ((rc = check_nd(lse, "lse", 3)) != DSV_OK) return rc;
+  if (lse->dtype != DSV_F32 || lse->shape[0] != B || lse->shape[1] != M || lse->shape[2] != H)
+    return fail(DSV_ERR_INVALID, "lse must be float32 [B, M, H]");
+  const Plan p = make_plan(B, M, H, Hk, D, N, 0, false);
+  if ((rc = check_ws(p, workspace, workspace_bytes)) != DSV_OK) return rc;
+
+  AttnArgs a{};
+  fill_common(a, q, Hk, p, workspace);
+  a.pre = dense_src(k, v, 0);
+  a.n_pre = N;
+  a.dmask = static_cast<const uint8_t*>(mask->data);
+  a.dm_sb = mask->shape[0] > 1 ? mask->stride[0] : 0;
+  a.dm_sm = mask->stride[1];
+  a.dm_sn = mask->stride[2];
+  a.dm_n = mask->shape[2];
+  MergeArgs m{};
+  fill_merge(m, a, out, (int)D);
+  m.lse = static_cast<float*>(lse->data);
+  m.l_sb = lse->stride[0];
+  m.l_sm = lse->stride[1];
+  m.l_sh = lse->stride[2];
+  return run(a, m, q->dtype, (int)D, true, static_cast<hipStream_t>(stream));
+}
+
+int dsv_verify_bundle_paged(const dsv_tensor* q, const dsv_tensor* kv_pages, const dsv_tensor* page_table,
+                            int64_t layer_idx, const dsv_tensor* mask, dsv_tensor* out, dsv_tensor* lse,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+  int rc;
+  if ((rc = check_q_out(q, out)) != DSV_OK) return rc;
+  const int64_t B = q->shape[0], M = q->shape[1], H = q->shape[2], D = q->shape[3];
+  KvSrc s{};
+  int64_t ps = 0, Hk = 0, Dk = 0, cap = 0;
+  if ((rc = paged_src(kv_pages, layer_idx, page_table, B, s, ps, Hk, Dk, cap)) != DSV_OK) return rc;
+  if (kv_pages->dtype != q->dtype) return fail(DSV_ERR_INVALID, "q and kv_pages must share a dtype");
+  if (Dk != D) return fail(DSV_ERR_INVALID, "kv_pages head_dim differs from q");
+  if (H % Hk != 0) return fail(DSV_ERR_INVALID, "query heads must be a multiple of kv_pages heads");
+  if ((rc = check_byte_mask(mask, B, M, "mask")) != DSV_OK) return rc;
+  const int64_t N = mask->shape[2];
+  if (N > cap) return fail(DSV_ERR_INVALID, "mask covers %lld tokens but the page table maps %lld", (long long)N, (long long)cap);
+  if ((rc = check_nd(lse, "lse", 3)) != DSV_OK) return rc;
+  if (lse->dtype != DSV_F32 || lse->shape[0] != B || lse->shape[1] != M || lse->shape[2] != H)
+    return fail(DSV_ERR_INVALID, "lse must be float32 [B, M, H]");
+  const Plan p = make_plan(B, M, H, Hk, D, N, ps, false);
+  if ((rc = check_ws(p, workspace, workspace_bytes)) != DSV_OK) return rc;
+
+  AttnArgs a{};
+  fill_common(a, q, Hk, p, workspace);
+  a.pre = s;
+  a.n_pre = N;
+  a.dmask = static_cast<const uint8_t*>(mask->data);
+  a.dm_sb = mask->shape[0] > 1 ? mask->stride[0] : 0;
+  a.dm_sm = mask->stride[1];
+  a.dm_sn = mask->stride[2];
+  a.dm_n = N;
+  MergeArgs m{};
+  fill_merge(m, a, out, (int)D);
+  m.lse = static_cast<float*>(lse->data);
+  m.l_sb = lse->stride[0];
+  m.l_sm = lse->stride[1];
+  m.l_sh = lse->stride[2];
+  return run(a, m, q->dtype, (int)D, true, static_cast<hipStream_t>(stream));
+}
+
+int dsv_tree_verify(const dsv_tensor* q, const dsv_tensor* k, const dsv_tensor* v, const dsv_tensor* page_table,
+                    int64_t n_prefix, const dsv_tensor* parent, const dsv_tensor* row_perm, dsv_tensor* out,
+                    dsv_tensor* lse, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc;
+  if ((rc = check_q_out(q, out)) != DSV_OK) return rc;
+  const int64_t B = q->shape[0], M = q->shape[1], H = q->shape[2], D = q->shape[3];
+  if (M > dsv::kTreeMaxM) return fail(DSV_ERR_UNSUPPORTED, "trees larger than %d nodes are not supported", dsv::kTreeMaxM);
+  if (n_prefix < 0) return fail(DSV_ERR_INVALID, "n_prefix must be >= 0");
+  KvSrc src{};
+  int64_t Hk = 0, ps = 0, cap = 0;
+  if (present(page_table)) {
+    // k, v: [P, Hk, ps, D] page-pool halves.
+    if ((rc = check_nd(k, "k_pages", 4)) != DSV_OK) return rc;
+    if ((rc = check_nd(v, "v_pages", 4)) != DSV_OK) return rc;
+    if ((rc = check_vec16(k, "k_pages")) != DSV_OK) return rc;
+    if ((rc = check_vec16(v, "v_pages")) != DSV_OK) return rc;
+    for (int i = 0; i < 4; ++i)
+      if (k->shape[i] != v->shape[i]) return fail(DSV_ERR_INVALID, "k_pages and v_pages shapes differ");
+    if (k->dtype != q->dtype || v->dtype != q->dtype) return fail(DSV_ERR_INVALID, "q and pages must share a dtype");
+    if (k->shape[3] != D) return fail(DSV_ERR_INVALID, "page head_dim differs from q");
+    ps = k->shape[2];
+    const int sh = log2_exact(ps);
+    if (sh < 0) return fail(DSV_ERR_UNSUPPORTED, "page_size %lld must be a power of two", (long long)ps);
+    if ((rc = check_nd(page_table, "page_table", page_table->ndim)) != DSV_OK) return rc;
+    if (page_table->ndim != 1 && page_table->ndim != 2) return fail(DSV_ERR_INVALID, "page_table must be 1-d or 2-d");
+    if (page_table->dtype != DSV_I32 && page_table->dtype != DSV_I64)
+      return fail(DSV_ERR_INVALID, "page_table must be int32 or int64");
+    if (page_table->ndim == 2 && page_table->shape[0] != B && page_table->shape[0] != 1)
+      return fail(DSV_ERR_INVALID, "page_table batch must be 1 or B");
+    if (page_table->stride[page_table->ndim - 1] != 1) return fail(DSV_ERR_INVALID, "page_table innermost stride must be 1");
+    Hk = k->shape[1];
+    src.k = static_cast<const uint16_t*>(k->data);
+    src.v = static_cast<const uint16_t*>(v->data);
+    src.k_sp = k->stride[0];
+    src.k_sh = k->stride[1];
+    src.k_st = k->stride[2];
+    src.v_sp = v->stride[0];
+    src.v_sh = v->stride[1];
+    src.v_st = v->stride[2];
+    src.pt = page_table->data;
+    src.pt_i64 = page_table->dtype == DSV_I64;
+    src.ps_shift = sh;
+    src.pt_sb = (page_table->ndim == 2 && page_table->shape[0] > 1) ? page_table->stride[0] : 0;
+    src.n_phys = k->shape[0];
+    cap = page_table->shape[page_table->ndim - 1] * ps;
+  } else {
+    if ((rc = check_kv_dense(k, v, q, "k_cache", "v_cache")) != DSV_OK) return rc;
+    Hk = k->shape[2];
+    src = dense_src(k, v, 0);
+    cap = k->shape[1];
+  }
+  if (H % Hk != 0) return fail(DSV_ERR_INVALID, "query heads must be a multiple of key heads");
+  if (n_prefix + M > cap)
+    return fail(DSV_ERR_INVALID, "cache holds %lld tokens, n_prefix + M = %lld", (long long)cap, (long long)(n_prefix + M));
+  if (parent == nullptr || (parent->ndim != 1 && parent->ndim != 2))
+    return fail(DSV_ERR_INVALID, "parent must be [M] or [B, M]");
+  if ((rc = check_nd(parent, "parent", parent->ndim)) != DSV_OK) return rc;
+  if (parent->dtype != DSV_I32 && parent->dtype != DSV_I64) return fail(DSV_ERR_INVALID, "parent must be int32 or int64");
+  if (parent->shape[parent->ndim - 1] != M) return fail(DSV_ERR_INVALID, "parent must have M entries per tree");
+  if (parent->ndim == 2 && parent->shape[0] != B && parent->shape[0] != 1)
+    return fail(DSV_ERR_INVALID, "parent batch must be 1 or B");
+  if (present(row_perm)) {
+    if ((rc = check_nd(row_perm, "row_perm", 1)) != DSV_OK) return rc;
+    if (row_perm->dtype != DSV_I32 || row_perm->shape[0] != M || row_perm->stride[0] != 1)
+      return fail(DSV_ERR_INVALID, "row_perm must be a contiguous int32 [M] permutation");
+  }
+  if (present(lse)) {
+    if ((rc = check_nd(lse, "lse", 3)) != DSV_OK) return rc;
+    if (lse->dtype != DSV_F32 || lse->shape[0] != B || lse->shape[1] != M || lse->shape[2] != H)
+      return fail(DSV_ERR_INVALID, "lse must be float32 [B, M, H]");
+  }
+  const Plan p = make_plan(B, M, H, Hk, D, n_prefix, ps, true);
+  if ((rc = check_ws(p, workspace, workspace_bytes)) != DSV_OK) return rc;
+
+  AttnArgs a{};
+  fill_common(a, q, Hk, p, workspace);
+  a.pre = src;
+  a.pre.key0 = 0;
+  a.n_pre = n_prefix;
+  a.has_tree = 1;
+  a.tree = src;
+  a.tree.key0 = n_prefix;
+  a.tpar = parent->data;
+  a.tpar_i64 = parent->dtype == DSV_I64;
+  a.tpar_sb = (parent->ndim == 2 && parent->shape[0] > 1) ? parent->stride[0] : 0;
+  a.tpar_sm = parent->stride[parent->ndim - 1];
+  a.row_perm = present(row_perm) ? static_cast<const int32_t*>(row_perm->data) : nullptr;
+  MergeArgs m{};
+  fill_merge(m, a, out, (int)D);
+  if (present(lse)) {
+    m.lse = static_cast<float*>(lse->data);
+    m.l_sb = lse->stride[0];
+    m.l_sm = lse->stride[1];
+    m.l_sh = lse->stride[2];
+  }
+  return run(a, m, q->dtype, (int)D, false, static_cast<hipStream_t>(stream));
+}
+
+// ----------------------------------------------------------------------------
+// Acceptance
+// ----------------------------------------------------------------------------
+
+static int64_t accept_chunk(int64_t V) {
+  (void)V;
+  return 16384;
+}
+
+size_t dsv_accept_workspace_bytes(int64_t T, int64_t M, int64_t V) {
+  if (T <= 0 || M <= 0 || V <= 0) return 0;
+  const int64_t ch = accept_chunk(V);
+  const int64_t nchunk = (V + ch - 1) / ch;
+  const size_t rows = (size_t)T * M * nchunk;
+  return align_up(rows * 16, 256) + align_up(rows * 4, 256);
+}
+
+int dsv_tree_accept(int mode, const dsv_tensor* logits, const dsv_tensor* draft, const dsv_tensor* parent,
+                    const dsv_tensor* pos, int64_t max_hops, float temperature, float posterior_threshold,
+                    float posterior_alpha, dsv_tensor* out_path, dsv_tensor* out_tokens, dsv_tensor* out_info,
+                    dsv_tensor* out_next, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc;
+  if (mode != DSV_ACCEPT_GREEDY && mode != DSV_ACCEPT_TYPICAL) return fail(DSV_ERR_INVALID, "unknown acceptance mode %d", mode);
+  if ((rc = check_nd(logits, "logits", 3)) != DSV_OK) return rc;
+  if (logits->dtype != DSV_BF16 && logits->dtype != DSV_F16 && logits->dtype != DSV_F32)
+    return fail(DSV_ERR_INVALID, "logits must be bf16, f16 or f32");
+  if (logits->stride[2] != 1) return fail(DSV_ERR_INVALID, "logits vocab stride must be 1");
+  const int64_t T = logits->shape[0], M = logits->shape[1], V = logits->shape[2];
+  if (M < 1 || M > 1024) return fail(DSV_ERR_UNSUPPORTED, "trees of %lld nodes are not supported (1..1024)", (long long)M);
+  if (V < 1 || V > 0x7fffffff) return fail(DSV_ERR_INVALID, "vocab size out of range");
+  if ((rc = check_nd(draft, "draft", 2)) != DSV_OK) return rc;
+  if (draft->dtype != DSV_I64 || draft->shape[0] != T || draft->shape[1] != M)
+    return fail(DSV_ERR_INVALID, "draft must be int64 [T, M]");
+  if ((rc = check_nd(parent, "parent", 2)) != DSV_OK) return rc;
+  if (parent->dtype != DSV_I64 || parent->shape[0] != T || parent->shape[1] != M - 1)
+    return fail(DSV_ERR_INVALID, "parent must be int64 [T, M-1]");
+  if (pos == nullptr || (pos->ndim != 1 && pos->ndim != 2)) return fail(DSV_ERR_INVALID, "pos must be [M] or [T, M]");
+  if ((rc = check_nd(pos, "pos", pos->ndim)) != DSV_OK) return rc;
+  if (pos->dtype != DSV_I64 || pos->shape[pos->ndim - 1] != M) return fail(DSV_ERR_INVALID, "pos must be int64 with M entries");
+  if (pos->ndim == 2 && pos->shape[0] != T && pos->shape[0] != 1) return fail(DSV_ERR_INVALID, "pos batch must be 1 or T");
+  if (max_hops < 0) return fail(DSV_ERR_INVALID, "max_hops must be >= 0");
+  if (mode == DSV_ACCEPT_TYPICAL && !(temperature > 0.f)) return fail(DSV_ERR_INVALID, "temperature must be > 0");
+  auto chk_out = [&](const dsv_tensor* t, const char* name, int64_t cols) -> int {
+    int r;
+    if ((r = check_nd(t, name, 2)) != DSV_OK) return r;
+    if (t->dtype != DSV_I64 || t->shape[0] != T || t->shape[1] != cols || t->stride[1] != 1)
+      return fail(DSV_ERR_INVALID, "%s must be contiguous int64 [T, %lld]", name, (long long)cols);
+    return DSV_OK;
+  };
+  if ((rc = chk_out(out_path, "out_path", M)) != DSV_OK) return rc;
+  if ((rc = chk_out(out_tokens, "out_tokens", M)) != DSV_OK) return rc;
+  if ((rc = chk_out(out_info, "out_info", 4)) != DSV_OK) return rc;
+  if (present(out_next) && (rc = chk_out(out_next, "out_next", M)) != DSV_OK) return rc;
+  const size_t need = dsv_accept_workspace_bytes(T, M, V);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(DSV_ERR_WORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace_bytes);
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0) return fail(DSV_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+
+  AcceptArgs a{};
+  a.mode = mode;
+  a.logits = logits->data;
+  a.l_dtype = logits->dtype;
+  a.l_st = logits->stride[0];
+  a.l_sm = logits->stride[1];
+  a.T = (int)T;
+  a.M = (int)M;
+  a.V = V;
+  a.chunk = accept_chunk(V);
+  a.nchunk = (int)((V + a.chunk - 1) / a.chunk);
+  a.draft = static_cast<const int64_t*>(draft->data);
+  a.d_st = draft->stride[0];
+  a.d_sm = draft->stride[1];
+  a.parent = static_cast<const int64_t*>(parent->data);
+  a.p_st = parent->stride[0];
+  a.p_sm = parent->stride[1];
+  a.pos = static_cast<const int64_t*>(pos->data);
+  a.pos_st = (pos->ndim == 2 && pos->shape[0] > 1) ? pos->stride[0] : 0;
+  a.pos_sm = pos->stride[pos->ndim - 1];
+  a.max_hops = (int)std::min<int64_t>(max_hops, 1 << 20);
+  a.inv_temp = mode == DSV_ACCEPT_TYPICAL ? 1.f / temperature : 1.f;
+  a.eps = posterior_threshold;
+  a.alpha = posterior_alpha;
+  const size_t rows = (size_t)T * M * a.nchunk;
+  a.rstat = static_cast<float4*>(workspace);
+  a.rstat2 = reinterpret_cast<float*>(static_cast<char*>(workspace) + align_up(rows * 16, 256));
+  a.out_path = static_cast<int64_t*>(out_path->data);
+  a.op_st = out_path->stride[0];
+  a.out_tok = static_cast<int64_t*>(out_tokens->data);
+  a.ot_st = out_tokens->stride[0];
+  a.out_info = static_cast<int64_t*>(out_info->data);
+  a.oi_st = out_info->stride[0];
+  if (present(out_next)) {
+    a.out_next = static_cast<int64_t*>(out_next->data);
+    a.on_st = out_next->stride[0];
+  }
+  hipEvent_t ev0, ev1;
+  take_events(ev0, ev1);
+  hipError_t e = dsv::launch_accept(a, static_cast<hipStream_t>(stream), ev0, ev1);
+  if (e != hipSuccess) return hip_fail(e, "acceptance kernel launch");
+  return DSV_OK;
+}
+
+}  // extern "C"

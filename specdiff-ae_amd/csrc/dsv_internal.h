@@ -1,0 +1,131 @@
+// dsv_internal.h — device-side types, helpers and launch-argument structs
+// shared by the gfx950 kernels and the C-ABI layer of libdsv.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dsv {
+
+// ---------------------------------------------------------------------------
+// Vector types used as MFMA operands / 16-byte memory transactions.
+// ---------------------------------------------------------------------------
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// Element-type tags (the kernels move 16-bit storage; the tag selects the
+// MFMA flavour and the fp32 -> 16-bit conversion of softmax probabilities).
+struct BF16 {};
+struct F16 {};
+
+// Limits of the in-kernel tables (checked by the host before launch).
+constexpr int kTileKeys = 64;        // keys per LDS tile
+constexpr int kPageLds = 1040;       // page-table entries staged per split
+constexpr int kTreeMaxM = 256;       // tree nodes handled by the tree split
+constexpr int kTreeMaxW = kTreeMaxM / 64;
+
+// A key/value source: contiguous [B, N, Hk, D] or a page pool half
+// [P, Hk, page, D] addressed through a page table.
+//   contiguous:  addr(b, n, h) = base + b*sb + (key0+n)*st + h*sh
+//   paged:       ln = key0+n; addr = base + b*sb + pt[b][ln>>ps]*sp + h*sh + (ln & (2^ps-1))*st
+struct KvSrc {
+  const uint16_t* k;
+  const uint16_t* v;
+  int64_t k_sb, k_sp, k_sh, k_st;
+  int64_t v_sb, v_sp, v_sh, v_st;
+  const void* pt;      // page table (nullptr -> contiguous)
+  int pt_i64;          // page table element is int64 (else int32)
+  int ps_shift;        // log2(page size)
+  int64_t pt_sb;       // page-table batch stride (0 -> shared by all batches)
+  int64_t key0;        // logical index of this source's key 0
+  int64_t n_phys;      // physical pages in the pool (page ids are clamped to it)
+};
+
+// Arguments of the split-K attention kernel (kernels 1 and 2).
+struct AttnArgs {
+  const uint16_t* q;
+  int64_t q_sb, q_sm, q_sh;
+  int B, M, H, Hk, G, R;   // R = G*M query rows per KV head
+  int n_rb;                // row blocks of 256 rows
+  float scale_log2;        // log2(e) / sqrt(D)
+
+  KvSrc pre;               // prefix source
+  int64_t n_pre;           // prefix keys [0, n_pre)
+  int n_splits;            // prefix splits
+  int64_t kps;             // prefix keys per split (multiple of kTileKeys)
+
+  // Optional byte mask [Bm, M, N] over the prefix keys (1 = keep).
+  const uint8_t* dmask;
+  int64_t dm_sb, dm_sm, dm_sn, dm_n;
+
+  // Optional tree split: keys [0, M) of `tree`, visibility = ancestor-or-self.
+  int has_tree;
+  KvSrc tree;
+  const void* tpar;        // parent array [B, M] (nullptr -> use tmask)
+  int tpar_i64;
+  int64_t tpar_sb, tpar_sm;
+  const void* tmask;       // dense M x M mask block (float additive or byte keep)
+  int tmask_dtype;         // dsv_dtype of tmask
+  int64_t tm_sb, tm_sm, tm_sn;
+
+  const int32_t* row_perm; // [M] node packing order (nullptr -> identity)
+
+  float* opart;            // [S, B, Hk, R, D] unnormalised partial outputs
+  float2* ml;              // [S, B, Hk, R] (running max in log2 units, sum)
+  int s_total;             // n_splits + has_tree
+};
+
+// Arguments of the LSE merge kernel (kernel 3).
+struct MergeArgs {
+  const float* opart;
+  const float2* ml;
+  int s_total;
+  int B, M, H, Hk, G, R, D;
+  const int32_t* row_perm;
+  void* out;               // [B, M, H, D] via strides
+  int out_dtype;
+  int64_t o_sb, o_sm, o_sh;
+  float* lse;              // optional, natural-log LSE at (b, m, h)
+  int64_t l_sb, l_sm, l_sh;
+  const float* plse;       // optional prefix LSE -> weight = sigmoid(plse - lse)
+  int64_t p_sb, p_sm, p_sh;
+  void* weight;            // [B, M, H] via strides, dtype = wdtype
+  int w_dtype;
+  int64_t w_sb, w_sm, w_sh;
+};
+
+// Arguments of the acceptance kernels (kernel 4).
+struct AcceptArgs {
+  int mode;                // 0 greedy, 1 typical
+  const void* logits;      // [T, M, V]
+  int l_dtype;
+  int64_t l_st, l_sm;      // tree, node strides (vocab stride 1)
+  int T, M;
+  int64_t V;
+  int nchunk;              // vocab chunks per row
+  int64_t chunk;           // elements per chunk
+  const int64_t* draft; int64_t d_st, d_sm;
+  const int64_t* parent; int64_t p_st, p_sm;
+  const int64_t* pos; int64_t pos_st, pos_sm;
+  int max_hops;
+  float inv_temp, eps, alpha;
+  float4* rstat;           // [T*M, nchunk] (argmax value, argmax index bits, m, l)
+  float* rstat2;           // [T*M, nchunk] s = sum y*e^(y-m) (typical)
+  int64_t* out_path; int64_t op_st;
+  int64_t* out_tok; int64_t ot_st;
+  int64_t* out_info; int64_t oi_st;
+  int64_t* out_next; int64_t on_st;
+};
+
+// ---------------------------------------------------------------------------
+// Launchers (defined in the .hip files, called by the C-ABI layer).
+// ---------------------------------------------------------------------------
+hipError_t launch_attn(const AttnArgs& a, int dtype, int D, bool dmask, hipStream_t s);
+hipError_t launch_merge(const MergeArgs& a, hipStream_t s);
+hipError_t launch_accept(const AcceptArgs& a, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1);
+
+}  // namespace dsv

@@ -1,0 +1,3 @@
+"""Host-side policies of the verification path."""
+
+from .bundle_scheduler import BundleScheduler, TreeDescriptorBuilder, bundle_row_order  # noqa: F401

@@ -1,0 +1,199 @@
+"""Tree acceptance on MI355X: the verify_new contract with a gfx950 acceptance kernel.
+
+Drop-in for ``verify`` / ``verify_new`` of the reference's
+``diffspec/draft/tree_verification.py`` (:66-257).  Lines :100-182 of the
+reference — per-node argmax, the ancestor closure, the deepest-node winner,
+the traceback and the next token — run in kernel 4 (libdsv.so), which
+returns the accepted path, its tokens and the next token in one small
+device buffer, read back with a single device-to-host copy instead of the
+reference's four (:112-118).  The remainder of verify_new (hazard tracker,
+tree budget, KV compaction, next-tree construction by the draft model, root
+prepend) follows the reference.
+
+Acceptance modes:
+  * ``greedy`` — the reference rule (``logits_processor is None``).
+  * ``typical`` — posterior (typical) acceptance of Cai et al. 2024 (Medusa):
+    accept node i iff p_T(draft[i] | parent) > min(eps, alpha * exp(-H)),
+    with H the entropy of p_T(. | parent); the reference has no such mode.
+The reference's multinomial sampling branch (``logits_processor`` given)
+draws from torch's RNG and is not reproduced; it raises.
+"""
+
+from __future__ import annotations
+
+from typing import Dict, Optional, Tuple
+
+import torch
+
+from .. import _ext
+from ..core.bundle_scheduler import BundleScheduler
+
+__all__ = ["tree_accept", "evaluate_tree", "verify", "verify_new"]
+
+
+def tree_accept(logits: torch.Tensor, draft: torch.Tensor, parent: torch.Tensor, pos: torch.Tensor,
+                max_hops: int, mode: str = "greedy", temperature: float = 1.0,
+                posterior_threshold: float = 0.09, posterior_alpha: float = 0.3,
+                return_next: bool = False) -> Dict[str, torch.Tensor]:
+    """Batched acceptance of T independent trees (kernel 4).
+
+    Args:
+        logits: [T, M, V] (or [M, V]) bf16/f16/f32 target logits per node.
+        draft: [T, M] int64 draft token per node (node 0 = root).
+        parent: [T, M-1] int64, reference convention (parent[k] is the parent
+            of node k+1 among non-root nodes; -1 or k itself = the root).
+        pos: [T, M] or [M] int64 position ids.
+        max_hops: closure rounds; the reference uses min(max_depth + 2, M).
+    Returns:
+        dict of device tensors: ``path`` [T, M] (node ids root..winner, then -1),
+        ``tokens`` [T, M], ``info`` [T, 4] = (winner, accept_length, next_token,
+        path_len or -1 on a malformed tree) and, if asked, ``next`` [T, M].
+    """
+    if logits.dim() == 2:
+        logits = logits.unsqueeze(0)
+    if draft.dim() == 1:
+        draft = draft.unsqueeze(0)
+    if parent.dim() == 1:
+        parent = parent.unsqueeze(0)
+    dev = _ext.require_gpu(logits, draft, parent, pos)
+    T, M, V = logits.shape
+    if draft.dtype != torch.int64:
+        draft = draft.to(torch.int64)
+    if parent.dtype != torch.int64:
+        parent = parent.to(torch.int64)
+    if pos.dtype != torch.int64:
+        pos = pos.to(torch.int64)
+    mode_id = {"greedy": _ext.ACCEPT_GREEDY, "typical": _ext.ACCEPT_TYPICAL}[mode]
+    lib = _ext.load()
+    path = torch.empty((T, M), dtype=torch.int64, device=dev)
+    tokens = torch.empty((T, M), dtype=torch.int64, device=dev)
+    info = torch.empty((T, 4), dtype=torch.int64, device=dev)
+    nxt = torch.empty((T, M), dtype=torch.int64, device=dev) if return_next else None
+    ws = _ext.workspace(lib.dsv_accept_workspace_bytes(T, M, V), dev)
+    rc = lib.dsv_tree_accept(mode_id, _ext.desc(logits), _ext.desc(draft), _ext.desc(parent), _ext.desc(pos),
+                             int(max_hops), float(temperature), float(posterior_threshold), float(posterior_alpha),
+                             _ext.desc(path), _ext.desc(tokens), _ext.desc(info), _ext.desc(nxt),
+                             ws.data_ptr(), ws.numel(), _ext.stream_of(dev))
+    _ext.check(rc, "tree_accept")
+    out = {"path": path, "tokens": tokens, "info": info}
+    if return_next:
+        out["next"] = nxt
+    return out
+
+
+def evaluate_tree(logits: torch.Tensor, draft: torch.Tensor, parent: torch.Tensor, position_ids: torch.Tensor,
+                  max_depth: int, mode: str = "greedy", temperature: float = 1.0,
+                  posterior_threshold: float = 0.09,
+                  posterior_alpha: float = 0.3) -> Tuple[list, list, int, torch.Tensor, int]:
+    """Lines :100-182 of verify_new for one tree.
+
+    Returns (best_candidate tokens, best_candidate node ids, accept_length,
+    next_token [1, 1] on the device, max_id).
+    """
+    M = draft.shape[-1]
+    pos = position_ids[0] if position_ids.dim() == 2 else position_ids
+    max_hops = min(int(max_depth) + 2, M)
+    r = tree_accept(logits.reshape(1, M, -1), draft.reshape(1, M), parent.reshape(1, M - 1), pos, max_hops,
+                    mode=mode, temperature=temperature, posterior_threshold=posterior_threshold,
+                    posterior_alpha=posterior_alpha)
+    host = torch.cat([r["info"], r["path"], r["tokens"]], dim=1).cpu()[0].tolist()
+    winner, accept_length, _, plen = host[:4]
+    if plen < 0:
+        raise RuntimeError("malformed draft tree: the parent chain does not reach the root")
+    ids = host[4:4 + plen]
+    toks = host[4 + M:4 + M + plen]
+    next_token = r["info"][:, 2:3]
+    return toks, ids, int(accept_length), next_token, int(winner)
+
+
+def verify(input_ids, logits, draft, position_ids, hidden_states, tree_attention_mask, past_key_values_data,
+           current_length_data, parent, model, nodes, threshold, max_depth, logits_processor, hazard_tracker=None):
+    """Redirects to verify_new (reference :66-72)."""
+    return verify_new(input_ids, logits, draft, position_ids, hidden_states, tree_attention_mask,
+                      past_key_values_data, current_length_data, parent, model, nodes, threshold, max_depth,
+                      logits_processor, hazard_tracker)
+
+
+@torch.no_grad()
+def verify_new(input_ids, logits, draft, position_ids, hidden_states, tree_attention_mask, past_key_values_data,
+               current_length_data, parent, model, nodes, threshold, max_depth, logits_processor,
+               hazard_tracker=None, acceptance: str = "greedy", temperature: float = 1.0,
+               posterior_threshold: float = 0.09, posterior_alpha: float = 0.3):
+    """Verify the draft tree and advance the generation state (reference :76-257).
+
+    Returns (input_ids, best_candidate, accept_length, next_draft,
+    next_position_ids, next_tree_attention_mask, next_parent).
+    """
+    if logits_processor is not None:
+        raise NotImplementedError(
+            "sampling verification (logits_processor) is not implemented by the MI355X kernels; "
+            "use acceptance='greedy' or acceptance='typical'")
+
+    # 1-2. Acceptance walk on the GPU (reference :100-182).
+    best_candidate, best_candidate_id, accept_length, next_token, max_id = evaluate_tree(
+        logits, draft, parent, position_ids, max_depth, mode=acceptance, temperature=temperature,
+        posterior_threshold=posterior_threshold, posterior_alpha=posterior_alpha)
+    next_token = next_token.to(draft.device)
+    pos_all = position_ids[0] if position_ids.dim() == 2 else position_ids
+
+    if getattr(model.draft_model, "enable_bundle_scheduling", False):
+        scheduler = getattr(model.draft_model, "bundle_scheduler", None)
+        if scheduler is None:
+            scheduler = BundleScheduler(bundle_size=3, max_bundles=100, device=str(draft.device))
+            model.draft_model.bundle_scheduler = scheduler
+        par = parent.detach().to("cpu").tolist()
+        parent_map = {0: -1}
+        for k, p in enumerate(par):
+            parent_map[k + 1] = (-1 if p == k else p) + 1
+        children = set(parent_map.values()) - {-1}
+        leaf_ids = [i for i in range(len(par) + 1) if i not in children]
+        pos_cpu = pos_all.detach().to("cpu").tolist()
+        depth_map = {i: int(pos_cpu[i]) for i in range(len(pos_cpu))}
+        bundles = scheduler.schedule_bundles({"leaf_ids": leaf_ids, "parent_map": parent_map,
+                                              "depth_map": depth_map}, return_tensors=False)
+        model.draft_model.last_bundle_stats = {"num_leaves": len(leaf_ids), "num_bundles": len(bundles),
+                                               "avg_prefix_length": scheduler.avg_prefix_length}
+
+    if hazard_tracker is not None:
+        observed_tree_depth = int(max(0, int((pos_all.max() - pos_all[0]).item())))
+        first_reject_depth = -1 if accept_length >= observed_tree_depth else int(accept_length)
+        hazard_tracker.update(first_reject_depth)
+
+    budget_controller = getattr(model, "tree_budget_controller", None)
+    next_nodes = int(nodes)
+    if budget_controller is not None:
+        next_nodes = budget_controller.observe(int(accept_length))
+    model.draft_model.last_tree_node_budget = next_nodes
+
+    # 3. Compact the accepted KV rows and update the cache length (reference :197-217).
+    start = int(current_length_data[0].item()) - int(draft.size(1))
+    select_indices = torch.tensor(best_candidate_id, device=input_ids.device, dtype=torch.long) + start
+    if getattr(model.draft_model, "use_retrieval_cache", False) and getattr(model.draft_model,
+                                                                             "retrieval_condition", False):
+        prev_input_len = input_ids.shape[1]
+        last_query_index = best_candidate_id[-1]
+        last_attn_scores = model.draft_model.attn_scores[:, :, last_query_index, :].mean(dim=1).squeeze()
+        abs_ids = torch.tensor(best_candidate_id, device=last_attn_scores.device) + prev_input_len
+        model.draft_model.attn_scores_final = torch.cat(
+            (last_attn_scores[:prev_input_len], last_attn_scores[abs_ids]), dim=0)
+    n_sel = len(best_candidate_id)
+    for data in past_key_values_data:
+        tgt = data[..., select_indices.to(data.device), :]
+        data[..., start:start + n_sel, :].copy_(tgt, non_blocking=True)
+    current_length_data.fill_(start + n_sel)
+
+    # 4. Append the accepted path and build the next draft tree (reference :219-257).
+    input_ids = torch.cat(
+        [input_ids, torch.tensor(best_candidate, device=input_ids.device, dtype=input_ids.dtype).unsqueeze(0)],
+        dim=-1)
+    new_accept_hidden = hidden_states[:, torch.tensor(best_candidate_id, device=hidden_states.device), :]
+    next_draft, next_position_ids, next_tree_attention_mask, next_parent = model.draft_model.build_speculative_tree(
+        new_accept_hidden, input_ids=torch.cat((input_ids, next_token.to(input_ids.device)), dim=1),
+        head=model.base_model.lm_head, nodes=next_nodes, threshold=threshold, max_depth=max_depth)
+    next_draft = torch.cat([next_token.to(next_draft.device), next_draft], dim=-1)
+    root_pos_val = (pos_all[max_id] + 1).to(next_position_ids.device)
+    next_position_ids = torch.cat([root_pos_val.view(1), next_position_ids], dim=-1)
+    m = next_tree_attention_mask
+    m = torch.cat([torch.zeros(1, m.size(1), dtype=m.dtype, device=m.device), m], dim=0)
+    m = torch.cat([torch.ones(m.size(0), 1, dtype=m.dtype, device=m.device), m], dim=1)
+    return input_ids, best_candidate, accept_length, next_draft, next_position_ids, m, next_parent

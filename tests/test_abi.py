@@ -1,0 +1,118 @@
+"""The C-ABI library (CPU-side checks only: no kernel is launched here).
+
+  * libdsv.so loads and exports every function include/dsv.h declares;
+  * the ctypes signature table matches the header;
+  * argument validation fails loudly with an error code and a message;
+  * the Python API refuses CPU tensors (no CPU fallback exists).
+"""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from diffspec_mi355x import _ext
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "dsv.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(dsv_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_expected_entry_points():
+    names = declared_functions()
+    for n in ["dsv_prefix_attention_forward", "dsv_tree_attention_forward", "dsv_verify_bundle",
+              "dsv_verify_bundle_paged", "dsv_tree_verify", "dsv_tree_accept", "dsv_last_error"]:
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol(dsv_lib):
+    for name in declared_functions():
+        assert hasattr(dsv_lib, name), f"{name} declared in dsv.h but not exported"
+        assert name in _ext.SIGNATURES, f"{name} has no ctypes signature"
+
+
+def test_version(dsv_lib):
+    assert dsv_lib.dsv_version() >= 1
+
+
+def test_workspace_sizes(dsv_lib):
+    # invalid arguments -> 0
+    assert dsv_lib.dsv_attn_workspace_bytes(1, 64, 30, 8, 128, 1000, 16, 1) == 0
+    n = dsv_lib.dsv_attn_workspace_bytes(1, 64, 32, 8, 128, 65536, 16, 1)
+    rows = 8 * 256
+    assert n >= 2 * rows * (128 * 4 + 8)  # at least one prefix split + the tree split
+    assert dsv_lib.dsv_accept_workspace_bytes(8, 64, 128256) >= 8 * 64 * 8 * 20
+
+
+def _t(shape, dtype=_ext.DSV_BF16, ptr=0x1000):
+    d = _ext.DsvTensor()
+    d.data = ptr
+    d.dtype = dtype
+    d.ndim = len(shape)
+    st = 1
+    for i in reversed(range(len(shape))):
+        d.shape[i] = shape[i]
+        d.stride[i] = st
+        st *= shape[i]
+    return d
+
+
+def test_validation_errors_are_reported(dsv_lib):
+    q = _t((1, 4, 8, 128))
+    k = _t((1, 16, 2, 128))
+    out = _t((1, 4, 8, 128))
+    lse_bad = _t((1, 4, 8), _ext.DSV_F32)  # should be [B, H, M] = (1, 8, 4)
+    rc = dsv_lib.dsv_prefix_attention_forward(ctypes.byref(q), ctypes.byref(k), ctypes.byref(k), -1,
+                                              ctypes.byref(out), ctypes.byref(lse_bad), None, 0, None)
+    assert rc == -1 and "lse" in _ext.last_error()
+    q32 = _t((1, 4, 8, 128), _ext.DSV_F32)
+    rc = dsv_lib.dsv_prefix_attention_forward(ctypes.byref(q32), ctypes.byref(k), ctypes.byref(k), -1,
+                                              ctypes.byref(out), ctypes.byref(lse_bad), None, 0, None)
+    assert rc == -2 and "bf16" in _ext.last_error()
+    q96 = _t((1, 4, 8, 96))
+    rc = dsv_lib.dsv_prefix_attention_forward(ctypes.byref(q96), ctypes.byref(k), ctypes.byref(k), -1,
+                                              ctypes.byref(q96), ctypes.byref(lse_bad), None, 0, None)
+    assert rc == -2 and "head_dim" in _ext.last_error()
+    lse = _t((1, 8, 4), _ext.DSV_F32)
+    rc = dsv_lib.dsv_prefix_attention_forward(ctypes.byref(q), ctypes.byref(k), ctypes.byref(k), -1,
+                                              ctypes.byref(out), ctypes.byref(lse), None, 0, None)
+    assert rc == -3 and "workspace" in _ext.last_error()
+
+
+def test_accept_validation(dsv_lib):
+    logits = _t((2, 8, 100), _ext.DSV_BF16)
+    draft = _t((2, 8), _ext.DSV_I64)
+    parent_bad = _t((2, 8), _ext.DSV_I64)  # must be [T, M-1]
+    pos = _t((8,), _ext.DSV_I64)
+    o = _t((2, 8), _ext.DSV_I64)
+    info = _t((2, 4), _ext.DSV_I64)
+    none = _ext.DsvTensor()
+    rc = dsv_lib.dsv_tree_accept(0, ctypes.byref(logits), ctypes.byref(draft), ctypes.byref(parent_bad),
+                                 ctypes.byref(pos), 10, 1.0, 0.09, 0.3, ctypes.byref(o), ctypes.byref(o),
+                                 ctypes.byref(info), ctypes.byref(none), None, 0, None)
+    assert rc == -1 and "parent" in _ext.last_error()
+    rc = dsv_lib.dsv_tree_accept(7, ctypes.byref(logits), ctypes.byref(draft), ctypes.byref(parent_bad),
+                                 ctypes.byref(pos), 10, 1.0, 0.09, 0.3, ctypes.byref(o), ctypes.byref(o),
+                                 ctypes.byref(info), ctypes.byref(none), None, 0, None)
+    assert rc == -1 and "mode" in _ext.last_error()
+
+
+def test_python_api_refuses_cpu_tensors(dsv_lib):
+    from diffspec_mi355x.runtime.tree_attention import prefix_attention_forward, tree_verify
+    from diffspec_mi355x.draft.tree_verification import tree_accept
+
+    q = torch.zeros(1, 4, 8, 64, dtype=torch.bfloat16)
+    k = torch.zeros(1, 16, 2, 64, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        prefix_attention_forward(q, k, k, 1, 4, 8, 64)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        tree_verify(q, k, k, 12, torch.tensor([-1, 0, 0, 1]))
+    with pytest.raises(RuntimeError, match="GPU only"):
+        tree_accept(torch.zeros(1, 4, 10), torch.zeros(1, 4, dtype=torch.long), torch.zeros(1, 3, dtype=torch.long),
+                    torch.arange(4), 4)

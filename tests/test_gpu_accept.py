@@ -1,0 +1,158 @@
+"""GPU parity of the acceptance kernel (4) against the oracle walk: accepted
+path, its tokens, accept length and next token must be bit-exact."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import accept as oacc
+from diffspec_mi355x import workloads as wl
+from diffspec_mi355x.draft.tree_verification import evaluate_tree, tree_accept, verify_new
+
+pytestmark = pytest.mark.gpu
+
+
+def run_and_compare(logits, draft, parent_ref, pos, max_depth, mode="greedy", **kw):
+    T, M = draft.shape
+    r = tree_accept(logits, draft, parent_ref, pos, min(max_depth + 2, M), mode=mode, return_next=True, **kw)
+    info = r["info"].cpu().numpy()
+    path = r["path"].cpu().numpy()
+    toks = r["tokens"].cpu().numpy()
+    lg = logits.float().cpu().numpy()
+    for t in range(T):
+        p = pos[t] if pos.dim() == 2 else pos
+        args = (lg[t], draft[t].cpu().numpy(), parent_ref[t].cpu().tolist(), p.cpu().numpy(), max_depth)
+        if mode == "greedy":
+            w_toks, w_ids, w_alen, w_next, w_id = oacc.greedy_walk(*args)
+        else:
+            w_toks, w_ids, w_alen, w_next, w_id = oacc.typical_walk(*args, **kw)
+        L = len(w_ids)
+        assert info[t].tolist() == [w_id, w_alen, w_next, L], f"tree {t}"
+        assert path[t, :L].tolist() == w_ids and (path[t, L:] == -1).all()
+        assert toks[t, :L].tolist() == w_toks and (toks[t, L:] == -1).all()
+        assert r["next"][t].cpu().tolist() == np.argmax(lg[t], axis=-1).tolist()
+    return info
+
+
+@pytest.mark.parametrize("mode", ["greedy", "typical"])
+def test_config4_bit_exact(gpu, mode):
+    """Config 4: 8 trees x 64 nodes, bf16 logits [8, 64, 128256] N(0, 3) with a
+    planted top token per node and a planted path of length 1..8."""
+    a = wl.make_accept_inputs(T=8, M=64, V=128256, device=str(gpu), pos_offset=1000)
+    kw = dict(temperature=1.0, posterior_threshold=0.09, posterior_alpha=0.3) if mode == "typical" else {}
+    info = run_and_compare(a.logits, a.draft, a.parent_ref, a.pos, 8, mode=mode, **kw)
+    assert all(info[t, 1] >= a.planted_len[t] for t in range(8))
+
+
+def test_typical_accepts_runner_up_that_greedy_rejects(gpu):
+    V, M = 5000, 6
+    lg = torch.full((1, M, V), -4.0)
+    lg[0, :, 10] = 3.0
+    lg[0, :, 11] = 2.9   # runner-up with high probability
+    lg[0, 2, 12] = 3.5   # node 2's distribution has a different top token
+    draft = torch.tensor([[0, 11, 10, 12, 11, 10]])
+    parent_ref = torch.tensor([[-1, 0, 1, -1, 3]])  # nodes 1..5 -> parents 0,1,2,0,4
+    pos = torch.tensor([0, 1, 2, 3, 1, 2])
+    kw = dict(temperature=1.0, posterior_threshold=0.09, posterior_alpha=0.3)
+    gi = run_and_compare(lg.to(torch.bfloat16).to(gpu), draft.to(gpu), parent_ref.to(gpu), pos.to(gpu), 8)
+    ti = run_and_compare(lg.to(torch.bfloat16).to(gpu), draft.to(gpu), parent_ref.to(gpu), pos.to(gpu), 8,
+                         mode="typical", **kw)
+    assert gi[0, 1] < ti[0, 1]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_logit_dtypes_and_vocab_tails(gpu, dtype):
+    # vocab not a multiple of the 16-byte vector width nor of the chunk size
+    a = wl.make_accept_inputs(T=3, M=40, V=16384 * 2 + 77, dtype=dtype, device=str(gpu), seed=5)
+    run_and_compare(a.logits, a.draft, a.parent_ref, a.pos, 8)
+    run_and_compare(a.logits, a.draft, a.parent_ref, a.pos, 8, mode="typical", temperature=0.7,
+                    posterior_threshold=0.09, posterior_alpha=0.3)
+
+
+def test_bf16_ties_take_first_index(gpu):
+    V, M = 40000, 4
+    lg = torch.zeros((1, M, V))
+    lg[0, :, [17, 39000, 20000]] = 5.0  # exact ties across vocab chunks
+    draft = torch.tensor([[0, 17, 17, 39000]])
+    parent_ref = torch.tensor([[-1, 0, 1]])
+    pos = torch.arange(M)
+    info = run_and_compare(lg.to(torch.bfloat16).to(gpu), draft.to(gpu), parent_ref.to(gpu), pos.to(gpu), 8)
+    assert info[0, 2] == 17 and info[0, 1] == 2
+
+
+def test_nan_ranks_first_like_torch_argmax(gpu):
+    V = 1000
+    lg = torch.randn((1, 3, V))
+    lg[0, 1, 500] = float("nan")
+    lg[0, 1, 700] = float("nan")
+    r = tree_accept(lg.to(gpu), torch.tensor([[0, 1, 2]], device=gpu), torch.tensor([[-1, 0]], device=gpu),
+                    torch.arange(3, device=gpu), 4, return_next=True)
+    assert r["next"][0].cpu().tolist() == torch.argmax(lg[0], -1).tolist()
+
+
+def test_bounded_closure_semantics(gpu):
+    M, V = 12, 64
+    lg = torch.zeros((1, M, V))
+    lg[0, :, 1] = 1
+    draft = torch.ones((1, M), dtype=torch.long)
+    draft[0, 1] = 2
+    parent_ref = torch.tensor([[-1] + list(range(M - 2))])
+    pos = torch.arange(M)
+    info = run_and_compare(lg.to(gpu), draft.to(gpu), parent_ref.to(gpu), pos.to(gpu), max_depth=2)
+    assert info[0, 0] == M - 1
+
+
+def test_malformed_parent_is_reported(gpu):
+    lg = torch.zeros((1, 4, 16), device=gpu)
+    r = tree_accept(lg, torch.zeros((1, 4), dtype=torch.long, device=gpu),
+                    torch.tensor([[-1, 7, 0]], device=gpu), torch.arange(4, device=gpu), 4)
+    assert r["info"][0, 3].item() == -1
+
+
+class _FakeDraftModel:
+    def __init__(self, dev):
+        self.dev = dev
+        self.enable_bundle_scheduling = True
+        self.use_retrieval_cache = False
+
+    def build_speculative_tree(self, hidden, input_ids, head, nodes, threshold, max_depth):
+        self.seen_input_ids = input_ids.clone()
+        d = torch.tensor([[5, 6, 7]], device=self.dev)
+        pos = torch.tensor([1, 2, 2], device=self.dev)
+        mask = torch.tensor([[1, 0, 0], [1, 1, 0], [1, 0, 1]], device=self.dev)
+        par = torch.tensor([-1, 0, 0], device=self.dev)
+        return d, pos, mask, par
+
+
+class _FakeModel:
+    def __init__(self, dev):
+        self.draft_model = _FakeDraftModel(dev)
+        self.base_model = type("B", (), {"lm_head": None})()
+
+
+def test_verify_new_contract_with_kv_compaction(gpu):
+    a = wl.make_accept_inputs(T=1, M=16, V=3000, device=str(gpu), seed=9, pos_offset=50)
+    M = 16
+    L = 80
+    kv = [torch.randn(2, 1, 2, L, 8, device=gpu) for _ in range(2)]
+    kv_before = [x.clone() for x in kv]
+    cur_len = torch.tensor([L - 4], dtype=torch.long)  # 60 prefix + 16 tree
+    start = L - 4 - M
+    input_ids = torch.arange(10, device=gpu).unsqueeze(0)
+    hidden = torch.randn(1, M, 4, device=gpu)
+    model = _FakeModel(gpu)
+    res = verify_new(input_ids, a.logits, a.draft, a.pos, hidden, None, kv, cur_len,
+                     a.parent_ref[0], model, nodes=3, threshold=0.1, max_depth=8, logits_processor=None)
+    ids_out, best, alen, nd, npos, nmask, npar = res
+    w = oacc.greedy_walk(a.logits[0].float().cpu().numpy(), a.draft[0].cpu().numpy(), a.parent_ref[0].tolist(),
+                         a.pos[0].cpu().numpy(), 8)
+    assert best == w[0] and alen == w[2]
+    assert ids_out[0, 10:].tolist() == w[0]
+    assert nd[0, 0].item() == w[3] and nd.shape == (1, 4)
+    assert npos[0].item() == int(a.pos[0, w[4]]) + 1
+    assert nmask.shape == (4, 4) and nmask[0].tolist() == [1, 0, 0, 0]
+    assert cur_len.item() == start + len(w[1])
+    sel = torch.tensor(w[1], device=gpu) + start
+    for x, x0 in zip(kv, kv_before):
+        assert torch.equal(x[..., start:start + len(w[1]), :], x0[..., sel, :])
+    assert model.draft_model.last_bundle_stats["num_bundles"] >= 1

@@ -1,0 +1,273 @@
+"""GPU parity of the attention kernels (1: split-K prefix, 2: tree block, 3: merge)
+against the float64 oracle on identical seeded inputs.
+
+Tolerances (attention outputs):
+  * max-abs 2e-2 and mean-abs 2e-3 against the fp32/fp64 computation;
+  * because that bar alone cannot see a zero output at 64K context (softmax is
+    nearly uniform there), every case also asserts a relative error
+    ||O - O*|| / ||O*|| <= 1e-2 (bf16 output) or 4e-3 (fp32 output) and a
+    natural-log LSE error <= 2e-3, and tree-only / short-prefix cases check
+    the tree block where it carries weight.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oa
+from diffspec_mi355x import workloads as wl
+from diffspec_mi355x.core.bundle_scheduler import bundle_row_order
+from diffspec_mi355x.runtime.bundle_verifier import FusedBundleVerifier, PagedBundleVerifier
+from diffspec_mi355x.runtime.tree_attention import prefix_attention_forward, tree_attention_forward, tree_verify
+
+pytestmark = pytest.mark.gpu
+
+
+def np64(t):
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+def assert_attn_close(got, want, rel=1e-2, max_abs=2e-2, mean_abs=2e-3, what=""):
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    diff = np.abs(got - want)
+    r = np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30)
+    assert diff.max() <= max_abs, f"{what} max-abs {diff.max():.3e}"
+    assert diff.mean() <= mean_abs, f"{what} mean-abs {diff.mean():.3e}"
+    assert r <= rel, f"{what} relative {r:.3e}"
+
+
+def assert_lse_close(got, want, tol=2e-3, what=""):
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    assert np.array_equal(np.isneginf(got), np.isneginf(want)), f"{what} -inf pattern differs"
+    fin = np.isfinite(want)
+    if fin.any():
+        err = np.abs(got[fin] - want[fin]).max()
+        assert err <= tol, f"{what} lse err {err:.3e}"
+
+
+def rand(shape, seed, dtype, dev, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * scale).to(dtype).to(dev)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D,H,Hk,M,N,B", [(128, 32, 8, 64, 1000, 2), (64, 8, 8, 10, 20, 1), (128, 32, 8, 5, 4096, 1),
+                                         (64, 16, 4, 33, 777, 1)])
+def test_prefix_attention_matches_oracle(gpu, dtype, D, H, Hk, M, N, B):
+    print(f"[prefix] dtype={dtype} D={D} H={H} Hk={Hk} M={M} N={N} B={B}", flush=True)
+    q, k, v = rand((B, M, H, D), 1, dtype, gpu), rand((B, N, Hk, D), 2, dtype, gpu), rand((B, N, Hk, D), 3, dtype, gpu)
+    out, lse = prefix_attention_forward(q, k, v, B, M, H, D)
+    torch.cuda.synchronize()
+    assert out.dtype == dtype and lse.shape == (B, H, M)
+    for b in range(B):
+        o_ref, l_ref = oa.prefix_attention(np64(q[b]), np64(k[b]), np64(v[b]))
+        assert_attn_close(np64(out[b]), o_ref, what=f"b={b}")
+        assert_lse_close(np64(lse[b]), l_ref, what=f"b={b}")
+
+
+def test_prefix_attention_expanded_kv_and_cache_seqlens(gpu):
+    B, M, H, D, N = 1, 16, 8, 128, 300
+    q = rand((B, M, H, D), 4, torch.bfloat16, gpu)
+    k2 = rand((B, N, 2, D), 5, torch.bfloat16, gpu)
+    v2 = rand((B, N, 2, D), 6, torch.bfloat16, gpu)
+    # repeat_kv-expanded form (H key heads) must equal the GQA form
+    ke = k2.repeat_interleave(4, dim=2)
+    ve = v2.repeat_interleave(4, dim=2)
+    o1, l1 = prefix_attention_forward(q, k2, v2, B, M, H, D)
+    o2, l2 = prefix_attention_forward(q, ke, ve, B, M, H, D)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(l1, l2)
+    from diffspec_mi355x.runtime.attention_compat import flash_attn_with_kvcache
+    o3, l3 = flash_attn_with_kvcache(q, k2, v2, causal=False, cache_seqlens=123, return_softmax_lse=True)
+    o_ref, l_ref = oa.prefix_attention(np64(q[0]), np64(k2[0, :123]), np64(v2[0, :123]))
+    assert_attn_close(np64(o3[0]), o_ref)
+    assert_lse_close(np64(l3[0]), l_ref)
+
+
+@pytest.mark.parametrize("mask_kind", ["float_additive", "int8", "bool", "bf16_additive"])
+def test_tree_attention_forward_matches_oracle(gpu, mask_kind):
+    B, M, H, Hk, D, T = 2, 64, 32, 8, 128, 70
+    print(f"[tree_attention_forward] mask={mask_kind}", flush=True)
+    q = rand((B, M, H, D), 7, torch.bfloat16, gpu)
+    k = rand((B, M, Hk, D), 8, torch.bfloat16, gpu)
+    v = rand((B, M, Hk, D), 9, torch.bfloat16, gpu)
+    parents = [wl.make_tree(M, seed=s)[0] for s in (3, 4)]
+    keep = np.stack([oa.ancestor_mask(p) for p in parents])
+    full = np.zeros((B, 1, T, T), dtype=bool)
+    full[:, 0, -M:, -M:] = keep
+    if mask_kind == "float_additive":
+        mask = torch.where(torch.from_numpy(full), 0.0, torch.finfo(torch.float32).min).to(gpu)
+    elif mask_kind == "bf16_additive":
+        mask = torch.where(torch.from_numpy(full), 0.0, -1e30).to(torch.bfloat16).to(gpu)
+    elif mask_kind == "int8":
+        mask = torch.from_numpy(full).to(torch.int8).to(gpu)
+    else:
+        mask = torch.from_numpy(full).to(gpu)
+    plse = (torch.randn(B, H, M) * 2 + 8).to(gpu)
+    cur, w, lse_t = tree_attention_forward(q, k, v, mask, 0, plse, B, M, H, D, return_lse=True)
+    torch.cuda.synchronize()
+    assert cur.shape == (B, M, H, D) and w.shape == (B, M, H, 1) and w.dtype == q.dtype
+    for b in range(B):
+        o_ref, w_ref, l_ref = oa.tree_attention(np64(q[b]), np64(k[b]), np64(v[b]), keep[b], np64(plse[b]))
+        assert_attn_close(np64(cur[b]), o_ref, what=f"b={b}")
+        assert_lse_close(np64(lse_t[b]), l_ref, what=f"b={b}")
+        np.testing.assert_allclose(np64(w[b])[..., 0], w_ref, atol=8e-3)
+
+
+def paged_case(gpu, n_prefix, M, H=32, Hk=8, D=128, seed=0, tree_seed=0, max_depth=8, max_outdeg=4):
+    return wl.make_tree_verify_inputs(n_prefix=n_prefix, M=M, H=H, Hk=Hk, D=D, seed=seed, tree_seed=tree_seed,
+                                      max_depth=max_depth, max_outdeg=max_outdeg, device=str(gpu))
+
+
+def oracle_tree_verify(inp, heads=None):
+    q = np64(inp.q[0])
+    k = np64(inp.logical_kv(0, 0)[0])
+    v = np64(inp.logical_kv(0, 1)[0])
+    if heads is not None:
+        H, Hk = q.shape[1], k.shape[1]
+        G = H // Hk
+        kv = sorted({h // G for h in heads})
+        assert [h for h in heads] == [x for kh in kv for x in range(kh * G, kh * G + G)]
+        q, k, v = q[:, heads], k[:, kv], v[:, kv]
+    return oa.tree_verify(q, k, v, inp.n_prefix, inp.parent)
+
+
+@pytest.mark.parametrize("n_prefix,M", [(4096, 64), (0, 64), (100, 7), (1000, 128), (16, 256)])
+def test_tree_verify_paged_matches_oracle(gpu, n_prefix, M):
+    print(f"[tree_verify paged] n_prefix={n_prefix} M={M}", flush=True)
+    inp = paged_case(gpu, n_prefix, M, tree_seed=n_prefix + M)
+    par = torch.tensor(inp.parent, dtype=torch.int64, device=gpu)
+    out, lse = tree_verify(inp.q, inp.kv_pages[0, 0], inp.kv_pages[0, 1], n_prefix, par, page_table=inp.page_table,
+                           out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    o_ref, l_ref = oracle_tree_verify(inp)
+    assert_attn_close(np64(out[0]), o_ref, rel=4e-3)
+    assert_lse_close(np64(lse[0]), l_ref)
+
+
+def test_tree_verify_dense_equals_paged_and_perm_invariant(gpu):
+    inp = paged_case(gpu, 3000, 64, tree_seed=5)
+    par = torch.tensor(inp.parent, dtype=torch.int32, device=gpu)
+    o_p, l_p = tree_verify(inp.q, inp.kv_pages[0, 0], inp.kv_pages[0, 1], 3000, par, page_table=inp.page_table)
+    kc, vc = inp.logical_kv(0, 0).contiguous(), inp.logical_kv(0, 1).contiguous()
+    o_d, l_d = tree_verify(inp.q, kc, vc, 3000, par)
+    perm = torch.tensor(bundle_row_order(inp.parent, num_bundles=8), dtype=torch.int32, device=gpu)
+    o_b, l_b = tree_verify(inp.q, inp.kv_pages[0, 0], inp.kv_pages[0, 1], 3000, par, page_table=inp.page_table,
+                           row_perm=perm)
+    torch.cuda.synchronize()
+    assert torch.equal(o_p, o_d) and torch.equal(l_p, l_d)
+    assert torch.equal(o_p, o_b) and torch.equal(l_p, l_b)
+
+
+@pytest.mark.parametrize("shape", ["chain", "star"])
+def test_tree_verify_special_trees(gpu, shape):
+    M, n_prefix = 32, 200
+    inp = paged_case(gpu, n_prefix, M, tree_seed=1)
+    inp.parent = [-1] + (list(range(M - 1)) if shape == "chain" else [0] * (M - 1))
+    par = torch.tensor(inp.parent, dtype=torch.int64, device=gpu)
+    out, lse = tree_verify(inp.q, inp.kv_pages[0, 0], inp.kv_pages[0, 1], n_prefix, par, page_table=inp.page_table,
+                           out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    o_ref, l_ref = oracle_tree_verify(inp)
+    assert_attn_close(np64(out[0]), o_ref, rel=4e-3)
+    assert_lse_close(np64(lse[0]), l_ref)
+
+
+def test_verify_bundle_reference_shapes_and_stats(gpu):
+    # reference tests/test_fused_kernel.py:19-27 shapes, now with numeric parity
+    ver = FusedBundleVerifier(bundle_size=3, enable_triton=True, device="cuda")
+    B, M, H, D, N = 1, 10, 8, 64, 20
+    q, k, v = rand((B, M, H, D), 11, torch.bfloat16, gpu), rand((B, N, H, D), 12, torch.bfloat16, gpu), \
+        rand((B, N, H, D), 13, torch.bfloat16, gpu)
+    mask = torch.tril(torch.ones(M, N, dtype=torch.int8, device=gpu))
+    o, lse = ver.verify_bundle(q, k, v, [mask, mask], shared_prefix_len=5)
+    torch.cuda.synchronize()
+    assert o.shape == q.shape and lse.shape == (B, M, H)
+    o_ref, l_ref = oa.masked_attention(np64(q[0]), np64(k[0]), np64(v[0]), mask.cpu().numpy() != 0)
+    assert_attn_close(np64(o[0]), o_ref)
+    assert_lse_close(np64(lse[0]), l_ref)
+    st = ver.get_statistics()
+    assert st["total_verifications"] == 2 and st["total_bundles"] == 1 and st["prefix_reuse_rate"] == 1
+
+
+def test_verify_bundle_fully_masked_row_and_paged_equivalence(gpu):
+    B, M, H, Hk, D, N, ps = 1, 12, 8, 2, 128, 300, 16
+    q = rand((B, M, H, D), 14, torch.bfloat16, gpu)
+    n_pages = (N + ps - 1) // ps
+    pool = rand((2, 2, n_pages + 3, Hk, ps, D), 15, torch.bfloat16, gpu)
+    pt = torch.from_numpy(np.random.default_rng(3).permutation(n_pages + 3)[:n_pages].astype(np.int64)).to(gpu)
+    mask = (torch.rand(M, N, generator=torch.Generator().manual_seed(4)) < 0.5).to(torch.int8)
+    mask[3] = 0  # fully masked row
+    mask = mask.to(gpu)
+    pv = PagedBundleVerifier(device="cuda")
+    o_p, l_p = pv.verify_bundle_paged(q, pool, pt, [mask], layer_idx=1)
+    tok = torch.arange(N, device=gpu)
+    k = pool[1, 0][pt[tok // ps], :, tok % ps].unsqueeze(0).contiguous()
+    v = pool[1, 1][pt[tok // ps], :, tok % ps].unsqueeze(0).contiguous()
+    o_d, l_d = pv.verify_bundle(q, k, v, [mask])
+    torch.cuda.synchronize()
+    assert torch.equal(o_p, o_d) and torch.equal(l_p, l_d)
+    assert torch.all(o_p[0, 3] == 0) and torch.all(torch.isneginf(l_p[0, 3]))
+    o_ref, l_ref = oa.masked_attention(np64(q[0]), np64(k[0]), np64(v[0]), mask.cpu().numpy() != 0)
+    assert_attn_close(np64(o_p[0]), o_ref)
+    assert_lse_close(np64(l_p[0]), l_ref)
+
+
+def test_config1_fp32_inputs_within_north_star_tolerance(gpu):
+    """Config 1 shapes (N=4096, M=64, GQA 32/8, D=128, N(0,1) fp32, seed 0): the
+    kernels take bf16, so the fp32 inputs are rounded on the host; the result
+    is compared with the fp32-input oracle."""
+    g = torch.Generator().manual_seed(0)
+    M, H, Hk, D, N = 64, 32, 8, 128, 4096
+    q = torch.randn(1, M, H, D, generator=g)
+    kp, vp = torch.randn(1, N, Hk, D, generator=g), torch.randn(1, N, Hk, D, generator=g)
+    kt, vt = torch.randn(1, M, Hk, D, generator=g), torch.randn(1, M, Hk, D, generator=g)
+    parent, _ = wl.make_tree(M, seed=0)
+    kc = torch.cat([kp, kt], 1).to(torch.bfloat16).to(gpu)
+    vc = torch.cat([vp, vt], 1).to(torch.bfloat16).to(gpu)
+    out, lse = tree_verify(q.to(torch.bfloat16).to(gpu), kc, vc, N, torch.tensor(parent, device=gpu),
+                           out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    o_ref, l_ref = oa.tree_verify(q[0].double().numpy(), torch.cat([kp, kt], 1)[0].double().numpy(),
+                                  torch.cat([vp, vt], 1)[0].double().numpy(), N, parent)
+    assert_attn_close(np64(out[0]), o_ref, rel=2e-2)
+    assert_lse_close(np64(lse[0]), l_ref, tol=5e-2)
+
+
+def test_config2_full_size_subset_heads(gpu):
+    """Config 2: 64K paged prefix, 64-node tree, bf16 N(0,1)*0.5; heads of KV heads 0-1 vs oracle."""
+    inp = paged_case(gpu, 65536, 64)
+    par = torch.tensor(inp.parent, dtype=torch.int64, device=gpu)
+    out, lse = tree_verify(inp.q, inp.kv_pages[0, 0], inp.kv_pages[0, 1], 65536, par, page_table=inp.page_table,
+                           out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    heads = list(range(8))
+    o_ref, l_ref = oracle_tree_verify(inp, heads)
+    assert_attn_close(np64(out[0, :, :8]), o_ref, rel=4e-3)
+    assert_lse_close(np64(lse[0, :, :8]), l_ref)
+    # the tree block alone (where the mask matters) on the same data
+    out_t, lse_t = tree_verify(inp.q, inp.kv_pages[0, 0], inp.kv_pages[0, 1], 0, par,
+                               page_table=inp.page_table[4096:], out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    q = np64(inp.q[0])[:, heads]
+    kt = np64(inp.logical_kv(0, 0)[0, 65536:])[:, :2]
+    vt = np64(inp.logical_kv(0, 1)[0, 65536:])[:, :2]
+    o_t, l_t = oa.masked_attention(q, kt, vt, oa.ancestor_mask(inp.parent))
+    assert_attn_close(np64(out_t[0, :, :8]), o_t, rel=4e-3)
+    assert_lse_close(np64(lse_t[0, :, :8]), l_t)
+
+
+def test_config3_bundle_packed_subset_heads(gpu):
+    """Config 3: 128K paged prefix, 128-node tree (depth <= 12, out-degree <= 6),
+    query rows packed in bundle order (8 bundles); KV head 0 vs oracle."""
+    inp = paged_case(gpu, 131072, 128, seed=2, tree_seed=2, max_depth=12, max_outdeg=6)
+    par = torch.tensor(inp.parent, dtype=torch.int64, device=gpu)
+    perm = torch.tensor(bundle_row_order(inp.parent, num_bundles=8), dtype=torch.int32, device=gpu)
+    out, lse = tree_verify(inp.q, inp.kv_pages[0, 0], inp.kv_pages[0, 1], 131072, par, page_table=inp.page_table,
+                           row_perm=perm, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    o_ref, l_ref = oracle_tree_verify(inp, list(range(4)))
+    assert_attn_close(np64(out[0, :, :4]), o_ref, rel=4e-3)
+    assert_lse_close(np64(lse[0, :, :4]), l_ref)
