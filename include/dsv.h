@@ -74,6 +74,19 @@ const char* dsv_last_error(void);
  */
 int dsv_set_timing_events(void* start_event, void* stop_event);
 
+/*
+ * Dry run (no reference counterpart; a safety check for callers and tests).
+ * While enabled on a thread, the attention entry points validate and plan as
+ * usual but launch nothing and touch no device memory: instead they walk
+ * every global and LDS address kernels 1-3 would access, with the kernels'
+ * own address arithmetic, and fail with DSV_ERR_INVALID naming the first
+ * access outside the extent of its argument (pointers are only compared,
+ * never dereferenced, so the call runs on machines without a GPU).
+ * dsv_dry_run_checks() returns the number of checks the last dry run made.
+ */
+int dsv_set_dry_run(int enable);
+int64_t dsv_dry_run_checks(void);
+
 /* ------------------------------------------------------------------------- */
 /* Attention (kernels 1-3: split-K flash-decoding, tree-ancestor block, merge) */
 /* ------------------------------------------------------------------------- */

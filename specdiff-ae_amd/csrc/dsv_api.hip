@@ -3,6 +3,7 @@
 // interface each entry point replaces are in include/dsv.h.
 
 #include "dsv.h"
+#include "dsv_check.h"
 #include "dsv_internal.h"
 
 #include <algorithm>
@@ -18,10 +19,36 @@ namespace {
 
 using dsv::AcceptArgs;
 using dsv::AttnArgs;
+using dsv::AttnExtents;
+using dsv::Extent;
 using dsv::KvSrc;
 using dsv::MergeArgs;
 
 thread_local std::string g_err;
+thread_local int g_dry_run = 0;
+thread_local int64_t g_dry_checks = 0;
+
+// Byte span of a tensor view from its data pointer (non-negative strides),
+// over dimensions [first, ndim).
+int64_t span_bytes(const dsv_tensor* t, int first = 0) {
+  int64_t s = 1;
+  for (int i = first; i < t->ndim; ++i) {
+    if (t->shape[i] == 0) return 0;
+    s += (t->shape[i] - 1) * t->stride[i];
+  }
+  static const int es[] = {2, 2, 4, 1, 1, 1, 4, 8};
+  return s * ((t->dtype >= 0 && t->dtype <= 7) ? es[t->dtype] : 1);
+}
+
+Extent extent_of(const char* name, const dsv_tensor* t) {
+  if (t == nullptr || t->ndim == 0 || t->data == nullptr) return Extent{name, 0, 0};
+  const uintptr_t lo = (uintptr_t)t->data;
+  return Extent{name, lo, lo + (uintptr_t)span_bytes(t)};
+}
+
+Extent extent_raw(const char* name, const void* p, int64_t bytes) {
+  return Extent{name, (uintptr_t)p, (uintptr_t)p + (uintptr_t)(bytes > 0 ? bytes : 0)};
+}
 
 int fail(int code, const char* fmt, ...) {
   char buf[512];
@@ -63,8 +90,10 @@ int check_nd(const dsv_tensor* t, const char* name, int ndim) {
     return fail(DSV_ERR_INVALID, "%s must be a %d-d tensor (got %d-d)", name, ndim, t ? t->ndim : -1);
   if (t->data == nullptr) return fail(DSV_ERR_INVALID, "%s has a null data pointer", name);
   if (elem_size(t->dtype) == 0) return fail(DSV_ERR_INVALID, "%s has an unknown dtype %d", name, t->dtype);
-  for (int i = 0; i < ndim; ++i)
+  for (int i = 0; i < ndim; ++i) {
     if (t->shape[i] < 0) return fail(DSV_ERR_INVALID, "%s has a negative extent", name);
+    if (t->stride[i] < 0) return fail(DSV_ERR_INVALID, "%s has a negative stride", name);
+  }
   return DSV_OK;
 }
 
@@ -104,20 +133,21 @@ struct Plan {
   size_t opart_bytes = 0, ml_bytes = 0, total = 0;
 };
 
-constexpr int kRowsPerBlock = 256;
-
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
+// Splits are sized so that prefix workgroups plus the tree workgroups fill
+// every resident workgroup slot of the GPU exactly once.
 Plan make_plan(int64_t B, int64_t M, int64_t H, int64_t Hk, int64_t D, int64_t n_keys, int64_t page_size,
                bool has_tree) {
   Plan p;
+  const int rows_per_block = dsv::attn_rows_per_block();
   p.G = (int)(H / Hk);
   p.R = (int)(p.G * M);
-  p.n_rb = (int)((p.R + kRowsPerBlock - 1) / kRowsPerBlock);
+  p.n_rb = (int)((p.R + rows_per_block - 1) / rows_per_block);
   const int64_t units = B * Hk * p.n_rb;
   if (n_keys > 0) {
-    const int64_t cus = device_cus();
-    const int64_t avail = std::max<int64_t>(cus - (has_tree ? units : 0), units);
+    const int64_t slots = (int64_t)device_cus() * dsv::attn_blocks_per_cu();
+    const int64_t avail = std::max<int64_t>(slots - (has_tree ? units : 0), units);
     const int64_t s0 = std::max<int64_t>(1, avail / units);
     int64_t kps_max = 16384;
     if (page_size > 0) kps_max = std::min<int64_t>(kps_max, (int64_t)(dsv::kPageLds - 2) * page_size);
@@ -129,7 +159,7 @@ Plan make_plan(int64_t B, int64_t M, int64_t H, int64_t Hk, int64_t D, int64_t n
   }
   p.s_total = p.n_splits + (has_tree ? 1 : 0);
   const size_t rows = (size_t)p.s_total * B * Hk * p.R;
-  p.opart_bytes = align_up(rows * D * sizeof(float), 256);
+  p.opart_bytes = align_up(rows * D * sizeof(uint16_t), 256);
   p.ml_bytes = align_up(rows * sizeof(float2), 256);
   p.total = p.opart_bytes + p.ml_bytes;
   return p;
@@ -189,6 +219,8 @@ KvSrc dense_src(const dsv_tensor* k, const dsv_tensor* v, int64_t key0) {
   s.v_sh = v->stride[2];
   s.pt = nullptr;
   s.key0 = key0;
+  s.k_bytes = span_bytes(k);
+  s.v_bytes = span_bytes(v);
   return s;
 }
 
@@ -216,7 +248,7 @@ void fill_common(AttnArgs& a, const dsv_tensor* q, int64_t Hk, const Plan& p, vo
   a.n_splits = p.n_splits;
   a.kps = p.kps;
   a.s_total = p.s_total;
-  a.opart = static_cast<float*>(ws);
+  a.opart = static_cast<uint16_t*>(ws);
   a.ml = reinterpret_cast<float2*>(static_cast<char*>(ws) + p.opart_bytes);
 }
 
@@ -249,7 +281,25 @@ void take_events(hipEvent_t& s, hipEvent_t& e) {
   g_ev_start = g_ev_stop = nullptr;
 }
 
-int run(const AttnArgs& a, const MergeArgs& m, int dtype, int D, bool dmask, hipStream_t st) {
+// Extents shared by every attention entry point (dry-run checks).
+AttnExtents common_extents(const dsv_tensor* q, const dsv_tensor* out, void* ws, const Plan& p) {
+  AttnExtents ex;
+  ex.q = extent_of("q", q);
+  ex.out = extent_of("out", out);
+  ex.ws = extent_raw("workspace", ws, (int64_t)p.total);
+  return ex;
+}
+
+int run(const AttnArgs& a, const MergeArgs& m, int dtype, int D, bool dmask, hipStream_t st,
+        const AttnExtents& ex) {
+  if (g_dry_run) {
+    std::string err;
+    int64_t n = 0;
+    const int rc = dsv::emulate_attention(a, m, D, dmask, ex, err, &n);
+    g_dry_checks = n;
+    if (rc != 0) return fail(DSV_ERR_INVALID, "dry run: out-of-bounds access: %s", err.c_str());
+    return DSV_OK;
+  }
   hipEvent_t ev0, ev1;
   take_events(ev0, ev1);
   if (ev0 != nullptr && hipEventRecord(ev0, st) != hipSuccess) return fail(DSV_ERR_HIP, "hipEventRecord(start) failed");
@@ -304,6 +354,7 @@ int paged_src(const dsv_tensor* kv_pages, int64_t layer, const dsv_tensor* pt, i
   s.pt_sb = (pt->ndim == 2 && pt->shape[0] > 1) ? pt->stride[0] : 0;
   s.key0 = 0;
   s.n_phys = kv_pages->shape[2];
+  s.k_bytes = s.v_bytes = span_bytes(kv_pages, 2);
   capacity = npt * page_size;
   (void)B;
   return DSV_OK;
@@ -322,6 +373,13 @@ int dsv_set_timing_events(void* start_event, void* stop_event) {
   g_ev_stop = static_cast<hipEvent_t>(stop_event);
   return DSV_OK;
 }
+
+int dsv_set_dry_run(int enable) {
+  g_dry_run = enable != 0;
+  return DSV_OK;
+}
+
+int64_t dsv_dry_run_checks(void) { return g_dry_checks; }
 
 size_t dsv_attn_workspace_bytes(int64_t B, int64_t M, int64_t H, int64_t Hk, int64_t D, int64_t n_keys,
                                 int64_t page_size, int has_tree) {
@@ -355,7 +413,11 @@ int dsv_prefix_attention_forward(const dsv_tensor* q, const dsv_tensor* k, const
   m.l_sb = lse->stride[0];
   m.l_sh = lse->stride[1];
   m.l_sm = lse->stride[2];
-  return run(a, m, q->dtype, (int)D, false, static_cast<hipStream_t>(stream));
+  AttnExtents ex = common_extents(q, out, workspace, p);
+  ex.pre_k = extent_of("k", k);
+  ex.pre_v = extent_of("v", v);
+  ex.lse = extent_of("lse", lse);
+  return run(a, m, q->dtype, (int)D, false, static_cast<hipStream_t>(stream), ex);
 }
 
 int dsv_tree_attention_forward(const dsv_tensor* q, const dsv_tensor* k, const dsv_tensor* v,
@@ -421,7 +483,14 @@ int dsv_tree_attention_forward(const dsv_tensor* q, const dsv_tensor* k, const d
   m.w_sb = weight->stride[0];
   m.w_sm = weight->stride[1];
   m.w_sh = weight->stride[2];
-  return run(a, m, q->dtype, (int)D, false, static_cast<hipStream_t>(stream));
+  AttnExtents ex = common_extents(q, current_out, workspace, p);
+  ex.tree_k = extent_of("key_states", k);
+  ex.tree_v = extent_of("value_states", v);
+  ex.tmask = extent_of("tree_mask", tree_mask);
+  ex.lse = extent_of("tree_lse", tree_lse);
+  ex.plse = extent_of("prefix_lse", prefix_lse);
+  ex.weight = extent_of("weight", weight);
+  return run(a, m, q->dtype, (int)D, false, static_cast<hipStream_t>(stream), ex);
 }
 
 int dsv_verify_bundle(const dsv_tensor* q, const dsv_tensor* k, const dsv_tensor* v, const dsv_tensor* mask,
@@ -453,7 +522,12 @@ int dsv_verify_bundle(const dsv_tensor* q, const dsv_tensor* k, const dsv_tensor
   m.l_sb = lse->stride[0];
   m.l_sm = lse->stride[1];
   m.l_sh = lse->stride[2];
-  return run(a, m, q->dtype, (int)D, true, static_cast<hipStream_t>(stream));
+  AttnExtents ex = common_extents(q, out, workspace, p);
+  ex.pre_k = extent_of("k", k);
+  ex.pre_v = extent_of("v", v);
+  ex.dmask = extent_of("mask", mask);
+  ex.lse = extent_of("lse", lse);
+  return run(a, m, q->dtype, (int)D, true, static_cast<hipStream_t>(stream), ex);
 }
 
 int dsv_verify_bundle_paged(const dsv_tensor* q, const dsv_tensor* kv_pages, const dsv_tensor* page_table,
@@ -492,7 +566,13 @@ int dsv_verify_bundle_paged(const dsv_tensor* q, const dsv_tensor* kv_pages, con
   m.l_sb = lse->stride[0];
   m.l_sm = lse->stride[1];
   m.l_sh = lse->stride[2];
-  return run(a, m, q->dtype, (int)D, true, static_cast<hipStream_t>(stream));
+  AttnExtents ex = common_extents(q, out, workspace, p);
+  ex.pre_k = extent_raw("kv_pages[layer, 0]", s.k, s.k_bytes);
+  ex.pre_v = extent_raw("kv_pages[layer, 1]", s.v, s.v_bytes);
+  ex.pre_pt = extent_of("page_table", page_table);
+  ex.dmask = extent_of("mask", mask);
+  ex.lse = extent_of("lse", lse);
+  return run(a, m, q->dtype, (int)D, true, static_cast<hipStream_t>(stream), ex);
 }
 
 int dsv_tree_verify(const dsv_tensor* q, const dsv_tensor* k, const dsv_tensor* v, const dsv_tensor* page_table,
@@ -539,6 +619,8 @@ int dsv_tree_verify(const dsv_tensor* q, const dsv_tensor* k, const dsv_tensor* 
     src.ps_shift = sh;
     src.pt_sb = (page_table->ndim == 2 && page_table->shape[0] > 1) ? page_table->stride[0] : 0;
     src.n_phys = k->shape[0];
+    src.k_bytes = span_bytes(k);
+    src.v_bytes = span_bytes(v);
     cap = page_table->shape[page_table->ndim - 1] * ps;
   } else {
     if ((rc = check_kv_dense(k, v, q, "k_cache", "v_cache")) != DSV_OK) return rc;
@@ -590,7 +672,14 @@ int dsv_tree_verify(const dsv_tensor* q, const dsv_tensor* k, const dsv_tensor* 
     m.l_sm = lse->stride[1];
     m.l_sh = lse->stride[2];
   }
-  return run(a, m, q->dtype, (int)D, false, static_cast<hipStream_t>(stream));
+  AttnExtents ex = common_extents(q, out, workspace, p);
+  ex.pre_k = ex.tree_k = extent_raw("k", src.k, src.k_bytes);
+  ex.pre_v = ex.tree_v = extent_raw("v", src.v, src.v_bytes);
+  ex.pre_pt = ex.tree_pt = extent_of("page_table", page_table);
+  ex.tpar = extent_of("parent", parent);
+  ex.perm = extent_of("row_perm", row_perm);
+  ex.lse = extent_of("lse", lse);
+  return run(a, m, q->dtype, (int)D, false, static_cast<hipStream_t>(stream), ex);
 }
 
 // ----------------------------------------------------------------------------

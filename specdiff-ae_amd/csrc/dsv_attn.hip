@@ -8,23 +8,33 @@
 //     (or filtered by a byte mask for the bundle-verifier contract), or
 //   * the tree split: the M tree keys, filtered by an ancestor-or-self bitmask
 //     built in LDS from the parent array (or from a dense mask block).
-// Each split writes an unnormalised partial (O, running max, running sum);
+// Each split writes a normalised bf16 partial O and its (running max, sum);
 // kernel 3 (dsv_merge.hip) combines the splits.
 //
-// Math per 64-key tile, per wave of WR rows (WR = 32 or 64):
+// Data movement per 32-key tile: K and V rows go HBM -> LDS by LDS-DMA
+// (buffer_load_dwordx4 ... lds), one 1 KiB wave-instruction per 4 keys, into
+// a 4-stage LDS ring (three tiles in flight while one is consumed; the ring
+// stays below 64 KiB).  Each lane's global chunk is chosen so that the LDS
+// image is XOR-swizzled for conflict-free operand reads.  The fast path
+// resolves the page once per instruction into a scalar base wrapped in a
+// buffer resource whose range ends at the tensor's end, so the hardware
+// bounds-checks every lane.  Address arithmetic lives in dsv_attn_geo.h and
+// is shared with the host-side emulation used by the dry-run mode.
+//
+// Math per tile, per wave of WR rows (WR = 32 or 64):
 //   S^T[key, row] = K[key, :] . Q[row, :]      v_mfma_f32_32x32x16_{bf16,f16}
 //   P = exp2(S * log2(e)/sqrt(D) - m_row)      online softmax, lazy rescale
 //   O^T[d, row]  += V^T[d, key] . P^T[key,row] v_mfma_f32_32x32x16_{bf16,f16}
-// Computing S^T (keys on the MFMA M side) leaves each lane owning one query
-// row and 16 keys in the accumulator, which is exactly the B-operand layout
-// the P.V product needs, so P never leaves registers.  V is transposed once
-// per tile while it is written to LDS, so the P.V A-operand is a single
-// 16-byte LDS read per lane.
+// S^T (keys on the MFMA M side) leaves each lane one query row and 16 keys:
+// exactly the B-operand layout of the P.V product, so P stays in registers;
+// the V^T A-operand comes straight from row-major V in LDS through
+// ds_read_b64_tr_b16 (16-lane block transpose).
 //
 // Reference semantics followed: runtime/tree_attention.py:116-217 (prefix
 // O + LSE with an online softmax), :220-292 (tree block), :40-63 (naive tree
 // attention), runtime/bundle_verifier.py:26-135 (masked bundle attention).
 
+#include "dsv_attn_geo.h"
 #include "dsv_internal.h"
 
 namespace dsv {
@@ -33,8 +43,12 @@ namespace {
 
 constexpr float kNegInf = -__builtin_huge_valf();
 // Lazy-rescale threshold in log2 units: the running max used for the
-// exponentials may lag the true max by up to this much (values <= 2^8).
+// exponentials may lag the true max by up to this much (p <= 2^8).
 constexpr float kRescaleTau = 8.0f;
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 template <typename T>
 __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c);
@@ -76,56 +90,92 @@ __device__ __forceinline__ float xor32_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-__device__ __forceinline__ u32x4 ld16(const uint16_t* p) {
-  return *reinterpret_cast<const u32x4*>(p);
-}
-
-// Physical 16-byte slot of head-dim index d inside a transposed V row:
-// a permutation inside each aligned group of 8, so that 16 consecutive lanes
-// reading consecutive d stay conflict-free while the transposing writes of
-// 16 lanes with different 8-wide d blocks spread over 8 slots.
-__device__ __forceinline__ int vt_phys(int d) { return (d & ~7) | ((d ^ (d >> 3)) & 7); }
+__device__ __forceinline__ u32x4 ld16(const uint16_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 
 __device__ __forceinline__ int64_t load_index(const void* p, int is64, int64_t i) {
   return is64 ? reinterpret_cast<const int64_t*>(p)[i] : (int64_t) reinterpret_cast<const int32_t*>(p)[i];
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// LDS-DMA: 16 bytes per lane, lane l lands at LDS m0 + 16*l.
+// Through a buffer resource (hardware range check; out-of-range lanes read 0).
+__device__ __forceinline__ void dma_buf(uint32_t lds, const void* base, uint32_t range, uint32_t voff) {
+  const uint64_t p = (uint64_t)base;
+  i32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)p);
+  r[1] = __builtin_amdgcn_readfirstlane((int)(uint32_t)(p >> 32));
+  r[2] = __builtin_amdgcn_readfirstlane((int)range);
+  r[3] = 0x00020000;
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(voff), "s"(r)
+               : "memory", "m0");
+}
+// With a full per-lane address (keys clamped to valid ones by the caller).
+__device__ __forceinline__ void dma_lane(uint32_t lds, const void* vaddr) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(vaddr) : "memory", "m0");
+}
+
+// Wait until at most N of this wave's vector-memory operations are pending.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier that the compiler may not move LDS accesses across and
+// that adds no memory-counter waits of its own (the DMA loads are waited for
+// explicitly with wait_vmcnt before it).
+__device__ __forceinline__ void barrier_lds() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 // Does element (i, j) of a dense tree-mask block keep the key?
 __device__ __forceinline__ bool tmask_keep(const AttnArgs& a, int b, int i, int j) {
   const int64_t off = b * a.tm_sb + i * a.tm_sm + j * a.tm_sn;
   switch (a.tmask_dtype) {
-    case 2: return reinterpret_cast<const float*>(a.tmask)[off] == 0.0f;          // f32 additive
-    case 0: return (reinterpret_cast<const uint16_t*>(a.tmask)[off] & 0x7fff) == 0; // bf16 additive (+-0 keep)
-    case 1: return (reinterpret_cast<const uint16_t*>(a.tmask)[off] & 0x7fff) == 0; // f16 additive
-    default: return reinterpret_cast<const uint8_t*>(a.tmask)[off] != 0;           // int8/uint8/bool
+    case 2: return reinterpret_cast<const float*>(a.tmask)[off] == 0.0f;            // f32 additive
+    case 0:                                                                          // bf16 additive
+    case 1: return (reinterpret_cast<const uint16_t*>(a.tmask)[off] & 0x7fff) == 0;  // f16 additive (+-0 keep)
+    default: return reinterpret_cast<const uint8_t*>(a.tmask)[off] != 0;             // int8/uint8/bool
   }
 }
 
+// Waves per SIMD: two for 32-row waves (8x32 layout, or two 4x32 workgroups
+// per CU), one for 64-row waves.
 template <typename T, int D, int NW, int WR, bool DMASK>
-__global__ void __launch_bounds__(NW * 64, NW / 4) attn_splitk_kernel(const AttnArgs a) {
+__global__ void __launch_bounds__(NW * 64, WR == 32 ? 2 : 1) attn_splitk_kernel(const AttnArgs a) {
+  using G = Geo<D>;
   constexpr int NT = NW * 64;
-  constexpr int KT = kTileKeys;
-  constexpr int KS = D / 16;   // k-steps of the Q.K^T product
-  constexpr int DT = D / 32;   // 32-row d tiles of the P.V product
-  constexpr int CH = D / 8;    // 16-byte chunks per key row
-  constexpr int SWZ = (CH < 16 ? CH : 16) - 1;
-  constexpr int RT = WR / 32;  // 32-row MFMA tiles per wave
-  constexpr int KCH = KT * CH;
-  constexpr int KLD = (KCH + NT - 1) / NT;
-  constexpr int VPR = (KT / 4) * CH;
-  constexpr int VLD = (VPR + NT - 1) / NT;
+  constexpr int KT = G::KT;
+  constexpr int KS = D / 16;                   // k-steps of the Q.K^T product
+  constexpr int DT = D / 32;                   // 32-row d tiles of the P.V product
+  constexpr int CH = G::CH;
+  constexpr int RT = WR / 32;                  // 32-row MFMA tiles per wave
+  constexpr int IPW = 2 * G::NINS / NW;        // DMA instructions per wave per tile
+  static_assert(IPW * NW == 2 * G::NINS, "tile DMA must split evenly over waves");
+  constexpr int PT_OFF = G::RING;
+  constexpr int VIS_OFF = PT_OFF + kPageLds * 4;
+  constexpr int LDS_BYTES = VIS_OFF + kTreeMaxM * kTreeMaxW * 8;
 
-  __shared__ __attribute__((aligned(16))) uint16_t ks_lds[2][KT * D];
-  __shared__ __attribute__((aligned(16))) uint16_t vt_lds[2][KT * D];
-  __shared__ int32_t pt_lds[kPageLds];
-  __shared__ uint64_t vis_lds[kTreeMaxM * kTreeMaxW];
+  // One LDS allocation so that the DMA ring sits at offset 0 (addresses < 64 KiB).
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[LDS_BYTES];
+  int32_t* pt_lds = reinterpret_cast<int32_t*>(smem + PT_OFF);
+  uint64_t* vis_lds = reinterpret_cast<uint64_t*>(smem + VIS_OFF);
 
   const int tid = threadIdx.x;
-  const int wid = tid >> 6, lane = tid & 63, lj = lane & 31, lg = lane >> 5;
+  // The wave index is uniform: readfirstlane lets every address derived from it
+  // live in SGPRs (scalar math) instead of being replicated per lane.
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63, lj = lane & 31, lg = lane >> 5;
 
-  // Block -> work item.  Consecutive dispatch ids go round-robin over the 8
-  // XCDs; remap so that neighbouring work items (row blocks of one split)
-  // land on the same XCD and share its L2.
+  // Block -> work item.  Dispatch ids go round-robin over the 8 XCDs; remap
+  // so that neighbouring work items (row blocks of one split) share an XCD.
   const int nblk = gridDim.x;
   int w = ((nblk & 7) == 0) ? (blockIdx.x & 7) * (nblk >> 3) + (blockIdx.x >> 3) : blockIdx.x;
   const int rb = w % a.n_rb;
@@ -145,21 +195,19 @@ __global__ void __launch_bounds__(NW * 64, NW / 4) attn_splitk_kernel(const Attn
     kstart = (int64_t)split * a.kps;
     kend = min(kstart + a.kps, a.n_pre);
   }
+  const int64_t nkeys = kend - kstart;
+  const int ntiles = nkeys > 0 ? (int)((nkeys + KT - 1) / KT) : 0;
+  const bool paged = src.pt != nullptr;
+  const int mode = dma_mode<D>(src);
 
-  // Stage this split's slice of the page table.
+  // ---- set-up: page-table slice, tree bitmask --------------------------------
   int64_t pt_lo = 0;
-  if (src.pt != nullptr && kend > kstart) {
+  if (paged && ntiles > 0) {
     pt_lo = (src.key0 + kstart) >> src.ps_shift;
     const int64_t pt_hi = (src.key0 + kend - 1) >> src.ps_shift;
-    for (int64_t i = tid; i <= pt_hi - pt_lo; i += NT) {
-      // Out-of-range entries are clamped so that no access leaves the pool.
-      int64_t pg = load_index(src.pt, src.pt_i64, b * src.pt_sb + pt_lo + i);
-      pg = pg < 0 ? 0 : (pg >= src.n_phys ? src.n_phys - 1 : pg);
-      pt_lds[i] = (int32_t)pg;
-    }
+    for (int64_t i = tid; i <= pt_hi - pt_lo; i += NT)
+      pt_lds[i] = (int32_t)clamp_page(load_index(src.pt, src.pt_i64, b * src.pt_sb + pt_lo + i), src.n_phys);
   }
-
-  // Tree split: ancestor-or-self bitmask of every node.
   if (is_tree) {
     const int M = a.M;
     for (int i = tid; i < M; i += NT) {
@@ -191,8 +239,41 @@ __global__ void __launch_bounds__(NW * 64, NW / 4) attn_splitk_kernel(const Attn
   }
   __syncthreads();
 
-  // This wave's query rows and their Q fragments (B operand of S^T = K.Q^T:
-  // lane (row lj, group lg) holds Q[row, 16*ks + 8*lg .. +8]).
+  // ---- DMA issue of one tile into its ring stage ------------------------------
+  // Instruction i covers keys [j*KPI, (j+1)*KPI) of the tile's K or V; lane p
+  // fills LDS bytes [16p, 16p+16) of that KiB = key j*KPI + p/CH, slot p%CH,
+  // which holds global chunk slot ^ swizzle(key).
+  const int kii = lane / CH;
+  const int slot = lane % CH;
+  auto issue_tile = [&](int t) {
+    const int stage = t & (G::STAGES - 1);
+    const int64_t kb = kstart + (int64_t)t * KT;
+#pragma unroll
+    for (int x = 0; x < IPW; ++x) {
+      bool is_v;
+      int j;
+      dma_ins<D>(wid * IPW + x, is_v, j);
+      const int key_t = j * G::KPI + kii;  // key within the tile
+      const int c = is_v ? v_slot(CH, key_t, slot) : k_slot(CH, key_t, slot);
+      const uint32_t dst = lds_addr(smem + (stage * 2 + (is_v ? 1 : 0)) * G::TILE + j * 1024);
+      const uint16_t* base = is_v ? src.v : src.k;
+      if (mode == kFast) {
+        const int64_t nb = fast_base_key(src, kb, kend, j, G::KPI);
+        const int64_t nl = fast_lane_key(src, kb, kend, j, G::KPI, kii);
+        const int64_t page = paged ? __builtin_amdgcn_readfirstlane(pt_lds[(nb >> src.ps_shift) - pt_lo]) : 0;
+        const int64_t be = src_elem(src, is_v, b, kvh, nb, page, 0);
+        const int64_t le = fast_lane_elem(src, is_v, nb, nl, c);
+        dma_buf(dst, base + be, rsrc_range(is_v ? src.v_bytes : src.k_bytes, be), (uint32_t)(le * 2));
+      } else {
+        const int64_t n = lane_key(src, kb, kend, key_t);
+        const int64_t page = paged ? pt_lds[(n >> src.ps_shift) - pt_lo] : 0;
+        dma_lane(dst, base + src_elem(src, is_v, b, kvh, n, page, c));
+      }
+    }
+  };
+
+  // ---- this wave's query rows: Q fragments (B operand of S^T = K.Q^T) --------
+  // lane (row lj, group lg) holds Q[row, 16*ks + 8*lg .. +8].
   const int row0 = rb * (NW * WR) + wid * WR;
   const bool wave_active = row0 < a.R;
   u32x4 qf[RT][KS];
@@ -228,203 +309,163 @@ __global__ void __launch_bounds__(NW * 64, NW / 4) attn_splitk_kernel(const Attn
     for (int dt = 0; dt < DT; ++dt) acc[rt][dt] = f32x16{};
   }
 
-  // Address of key n (source-relative) in the K or V half of the source.
-  auto kv_addr = [&](const uint16_t* base, int64_t sb, int64_t sp, int64_t sh, int64_t st,
-                     int64_t n) -> const uint16_t* {
-    const int64_t ln = src.key0 + n;
-    if (src.pt != nullptr) {
-      const int64_t page = pt_lds[(ln >> src.ps_shift) - pt_lo];
-      return base + b * sb + page * sp + kvh * sh + (ln & ((1ll << src.ps_shift) - 1)) * st;
-    }
-    return base + b * sb + ln * st + kvh * sh;
-  };
+  // Per-lane constant parts of the V^T operand reads (two transposed reads):
+  // 16-lane block bl = lane/16 holds d rows [16*(bl&1), +16) of a 32-row d
+  // tile and key group g = bl>>1; lane i of the block addresses key row
+  // 16*hh + 4*g + i/4 (+8 for the second read), columns d0 + 4*(i%4) .. +3.
+  const int bl = lane >> 4, bi = lane & 15;
+  const int vkey = 4 * (bl >> 1) + (bi >> 2);
+  const int vcol = 16 * (bl & 1) + 4 * (bi & 3);
 
-  u32x4 kreg[KLD];
-  u32x4 vreg[VLD][4];
-
-  auto load_tile = [&](int64_t kb) {
+  // ---- one tile of compute ---------------------------------------------------
+  auto compute = [&](const uint8_t* kt_lds, const uint8_t* vt_lds, int64_t kb, bool masked, int t) {
+    // ---- S^T = K . Q^T --------------------------------------------------------
+    f32x16 st[RT];
 #pragma unroll
-    for (int i = 0; i < KLD; ++i) {
-      const int c = tid + i * NT;
-      kreg[i] = u32x4{0, 0, 0, 0};
-      if (c < KCH) {
-        const int key = c / CH, ch = c % CH;
-        const int64_t n = kb + key;
-        if (n < kend) kreg[i] = ld16(kv_addr(src.k, src.k_sb, src.k_sp, src.k_sh, src.k_st, n) + ch * 8);
+    for (int rt = 0; rt < RT; ++rt) st[rt] = f32x16{};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const u32x4 kf = *reinterpret_cast<const u32x4*>(kt_lds + lj * (2 * D) + k_slot(CH, lj, 2 * ks + lg) * 16);
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) st[rt] = mfma32<T>(kf, qf[rt][ks], st[rt]);
+    }
+
+    // ---- masking (tail tiles, tree split, byte masks) -------------------------
+    // 16-bit keep mask per lane: bit v <-> key 4*lg + 8*(v/4) + v%4 of the tile.
+    if (masked) {
+      const int lim = (int)min(kend - kb, (int64_t)KT) - 4 * lg;  // valid keys from 4*lg
+      uint32_t tail = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int c = min(max(lim - 8 * q, 0), 4);  // valid keys among 8q .. 8q+3
+        tail |= ((1u << c) - 1u) << (4 * q);
       }
-    }
-#pragma unroll
-    for (int i = 0; i < VLD; ++i) {
-      const int p = tid + i * NT;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) vreg[i][e] = u32x4{0, 0, 0, 0};
-      if (p < VPR) {
-        const int qd = p / CH, dblk = p % CH;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int64_t n = kb + 4 * qd + e;
-          if (n < kend) vreg[i][e] = ld16(kv_addr(src.v, src.v_sb, src.v_sp, src.v_sh, src.v_st, n) + dblk * 8);
-        }
-      }
-    }
-  };
-
-  auto store_tile = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < KLD; ++i) {
-      const int c = tid + i * NT;
-      if (c < KCH) {
-        const int key = c / CH, ch = c % CH;
-        *reinterpret_cast<u32x4*>(&ks_lds[buf][key * D + ((ch ^ (key & SWZ)) * 8)]) = kreg[i];
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < VLD; ++i) {
-      const int p = tid + i * NT;
-      if (p < VPR) {
-        const int qd = p / CH, dblk = p % CH;
-        const int sb = qd >> 3;
-        const int kk = (qd & 7) * 4;
-        const int h = kk >> 4, r = kk & 15;
-        const int g = (r >> 2) & 1, e0 = (r >> 3) * 4;
-        uint16_t* base = &vt_lds[buf][((sb * 2 + h) * 2 + g) * D * 8 + e0];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int d = dblk * 8 + j;
-          const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
-          const uint32_t w01 = __builtin_amdgcn_perm(vreg[i][1][j >> 1], vreg[i][0][j >> 1], sel);
-          const uint32_t w23 = __builtin_amdgcn_perm(vreg[i][3][j >> 1], vreg[i][2][j >> 1], sel);
-          *reinterpret_cast<u32x2*>(base + vt_phys(d) * 8) = u32x2{w01, w23};
-        }
-      }
-    }
-  };
-
-  const int64_t nkeys = kend - kstart;
-  const int ntiles = nkeys > 0 ? (int)((nkeys + KT - 1) / KT) : 0;
-
-  if (ntiles > 0) {
-    load_tile(kstart);
-    store_tile(0);
-  }
-  __syncthreads();
-
-  for (int t = 0; t < ntiles; ++t) {
-    const int buf = t & 1;
-    const int64_t kb = kstart + (int64_t)t * KT;
-    if (t + 1 < ntiles) load_tile(kb + KT);
-
-    bool do_compute = wave_active;
-    uint64_t visw[RT];
-    if (is_tree) {
-      uint64_t any = 0;
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) {
-        visw[rt] = rvalid[rt] ? vis_lds[node_of[rt] * kTreeMaxW + t] : 0ull;
-        any |= visw[rt];
-      }
-      do_compute = do_compute && (__ballot(any != 0ull) != 0ull);
-    }
-
-    if (do_compute) {
-      // One 32-key subtile at a time: QK^T, mask, online softmax, PV.
-#pragma unroll
-      for (int sb = 0; sb < 2; ++sb) {
-        // ---- S^T = K . Q^T ----------------------------------------------
-        f32x16 st[RT];
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt) st[rt] = f32x16{};
-        const int key = sb * 32 + lj;
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) {
-          const int ch = ks * 2 + lg;
-          const u32x4 kf = *reinterpret_cast<const u32x4*>(&ks_lds[buf][key * D + ((ch ^ (key & SWZ)) * 8)]);
-#pragma unroll
-          for (int rt = 0; rt < RT; ++rt) st[rt] = mfma32<T>(kf, qf[rt][ks], st[rt]);
+        uint32_t keep = tail;
+        if (is_tree) {
+          // Visibility bits of this tile's keys, shifted to this lane's keys.
+          const uint64_t vw = rvalid[rt] ? vis_lds[node_of[rt] * kTreeMaxW + (t >> 1)] : 0ull;
+          const uint32_t vb = (uint32_t)(vw >> ((t & 1) * 32 + 4 * lg));
+          keep &= (vb & 0xFu) | ((vb >> 4) & 0xF0u) | ((vb >> 8) & 0xF00u) | ((vb >> 12) & 0xF000u);
         }
-
-        // ---- masking ----------------------------------------------------
-        // Lane (lj, lg) value v holds key sb*32 + 8*(v/4) + 4*lg + v%4.
-        if (kb + KT > kend || is_tree || DMASK) {
+        if constexpr (DMASK) {
+          const uint8_t* mrow = a.dmask + (int64_t)b * a.dm_sb + (int64_t)node_of[rt] * a.dm_sm;
+          const int64_t n0 = kb + 4 * lg;
+          uint32_t mb = 0;
 #pragma unroll
-          for (int rt = 0; rt < RT; ++rt) {
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-              const int kt = sb * 32 + 8 * (v >> 2) + 4 * lg + (v & 3);
-              const int64_t n = kb + kt;
-              bool keep = n < kend;
-              if (is_tree) keep = keep && ((visw[rt] >> kt) & 1ull);
-              if constexpr (DMASK) {
-                const int64_t mb = (int64_t)b * a.dm_sb + (int64_t)node_of[rt] * a.dm_sm;
-                keep = keep && (n < a.dm_n) && rvalid[rt] && (a.dmask[mb + n * a.dm_sn] != 0);
-              }
-              if (!keep) st[rt][v] = kNegInf;
-            }
+          for (int v = 0; v < 16; ++v) {
+            const int64_t n = n0 + 8 * (v >> 2) + (v & 3);
+            mb |= (uint32_t)((n < a.dm_n) && (mrow[n * a.dm_sn] != 0)) << v;
           }
+          keep &= rvalid[rt] ? mb : 0u;
         }
-
-        // ---- online softmax (log2 domain, lazy rescale) -----------------
-        float mt[RT];
-        bool need = false;
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-          float m0 = st[rt][0];
-#pragma unroll
-          for (int v = 1; v < 16; ++v) m0 = fmaxf(m0, st[rt][v]);
-          mt[rt] = xor32_max(m0) * a.scale_log2;
-          need = need || (mt[rt] > mx[rt] + kRescaleTau);
-        }
-        if (__ballot(need) != 0ull) {
-#pragma unroll
-          for (int rt = 0; rt < RT; ++rt) {
-            const float mn = fmaxf(mx[rt], mt[rt]);
-            const float al = (mn == mx[rt]) ? 1.f : __builtin_amdgcn_exp2f(mx[rt] - mn);
-            mx[rt] = mn;
-            lsum[rt] *= al;
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) acc[rt][dt] *= al;
-          }
-        }
-
-        u32x4 pk[RT][2];
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-          const float ms = (mx[rt] == kNegInf) ? 0.f : mx[rt];
-          float ls = 0.f;
-#pragma unroll
-          for (int hh = 0; hh < 2; ++hh) {
-            float p[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              p[e] = __builtin_amdgcn_exp2f(fmaf(st[rt][hh * 8 + e], a.scale_log2, -ms));
-              ls += p[e];
-            }
-            pk[rt][hh] = u32x4{pack2<T>(p[0], p[1]), pack2<T>(p[2], p[3]), pack2<T>(p[4], p[5]),
-                               pack2<T>(p[6], p[7])};
-          }
-          lsum[rt] += ls;
-        }
-
-        // ---- O^T += V^T . P^T -------------------------------------------
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-#pragma unroll
-          for (int dt = 0; dt < DT; ++dt) {
-            const int d = dt * 32 + lj;
-            const u32x4 vf = *reinterpret_cast<const u32x4*>(
-                &vt_lds[buf][(((sb * 2 + hh) * 2 + lg) * D + vt_phys(d)) * 8]);
-#pragma unroll
-            for (int rt = 0; rt < RT; ++rt) acc[rt][dt] = mfma32<T>(vf, pk[rt][hh], acc[rt][dt]);
-          }
-        }
+        for (int v = 0; v < 16; ++v) st[rt][v] = ((keep >> v) & 1u) ? st[rt][v] : kNegInf;
       }
     }
 
-    if (t + 1 < ntiles) store_tile(buf ^ 1);
-    __syncthreads();
+    // ---- online softmax (log2 domain, lazy rescale) ---------------------------
+    float mt[RT];
+    bool need = false;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      float m0 = fmaxf(st[rt][0], st[rt][1]);
+#pragma unroll
+      for (int v = 2; v < 16; v += 2) m0 = fmaxf(m0, fmaxf(st[rt][v], st[rt][v + 1]));
+      mt[rt] = xor32_max(m0) * a.scale_log2;
+      need = need || (mt[rt] > mx[rt] + kRescaleTau);
+    }
+    if (__ballot(need) != 0ull) {
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        const float mn = fmaxf(mx[rt], mt[rt]);
+        const float al = (mn == mx[rt]) ? 1.f : __builtin_amdgcn_exp2f(mx[rt] - mn);
+        mx[rt] = mn;
+        lsum[rt] *= al;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) acc[rt][dt] *= al;
+      }
+    }
+
+    u32x4 pk[RT][2];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const float ms = (mx[rt] == kNegInf) ? 0.f : mx[rt];
+      float ls = lsum[rt];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        uint32_t w4[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float p0 = __builtin_amdgcn_exp2f(fmaf(st[rt][hh * 8 + 2 * e], a.scale_log2, -ms));
+          const float p1 = __builtin_amdgcn_exp2f(fmaf(st[rt][hh * 8 + 2 * e + 1], a.scale_log2, -ms));
+          w4[e] = pack2<T>(p0, p1);
+          // The normaliser sums the unrounded probabilities: the LSE is an
+          // output in its own right and keeps fp32 accuracy.
+          ls += p0 + p1;
+        }
+        pk[rt][hh] = u32x4{w4[0], w4[1], w4[2], w4[3]};
+      }
+      lsum[rt] = ls;
+    }
+
+    // ---- O^T += V^T . P^T -----------------------------------------------------
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const int k0 = hh * 16 + vkey;  // first read: keys k0; second: k0 + 8
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const int col = dt * 32 + vcol;
+        const int c = col >> 3, cw = (col & 7) * 2;
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_s16x4*)(vt_lds + k0 * (2 * D) + v_slot(CH, k0, c) * 16 + cw));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_s16x4*)(vt_lds + (k0 + 8) * (2 * D) + v_slot(CH, k0 + 8, c) * 16 + cw));
+        const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+        const u32x4 vf = {l2[0], l2[1], h2[0], h2[1]};
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) acc[rt][dt] = mfma32<T>(vf, pk[rt][hh], acc[rt][dt]);
+      }
+    }
+  };
+
+  // ---- main loop over tiles: 4-stage DMA ring, one barrier per tile -----------
+  for (int t = 0; t < 3 && t < ntiles; ++t) issue_tile(t);
+  for (int t = 0; t < ntiles; ++t) {
+    // Tile t's loads are the oldest outstanding ones of this wave; the
+    // (up to two) newer issued tiles may stay in flight.
+    const int newer = min(ntiles - 1 - t, 2);
+    if (newer >= 2)
+      wait_vmcnt<2 * IPW>();
+    else if (newer == 1)
+      wait_vmcnt<IPW>();
+    else
+      wait_vmcnt<0>();
+    barrier_lds();  // tile t landed for every wave; every wave finished tile t-1
+    if (t + 3 < ntiles) issue_tile(t + 3);
+    const int stage = t & (G::STAGES - 1);
+    const int64_t kb = kstart + (int64_t)t * KT;
+    if (wave_active) {
+      bool do_compute = true;
+      if (is_tree) {
+        uint64_t any = 0;
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+          const uint64_t vw = rvalid[rt] ? vis_lds[node_of[rt] * kTreeMaxW + (t >> 1)] : 0ull;
+          any |= (vw >> ((t & 1) * 32)) & 0xffffffffull;
+        }
+        do_compute = __ballot(any != 0ull) != 0ull;
+      }
+      if (do_compute) {
+        // One compute body; masking is a short uniform branch inside it.
+        const bool masked = is_tree || DMASK || (kb + KT > kend);
+        compute(smem + stage * 2 * G::TILE, smem + (stage * 2 + 1) * G::TILE, kb, masked, t);
+      }
+    }
   }
 
-  // ---- epilogue: unnormalised partial + (max, sum) per row ----------------
+  // ---- epilogue: normalised bf16 partial + (max, sum) per row ----------------
   if (!wave_active) return;
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
@@ -432,57 +473,73 @@ __global__ void __launch_bounds__(NW * 64, NW / 4) attn_splitk_kernel(const Attn
     const int r = row0 + rt * 32 + lj;
     if (!rvalid[rt]) continue;
     const int64_t prow = (((int64_t)split * a.B + b) * a.Hk + kvh) * a.R + r;
-    float* op = a.opart + prow * D;
+    const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
+    uint16_t* op = a.opart + prow * D;
     // Accumulator value v of d tile dt holds d = 32*dt + 8*(v/4) + 4*lg + v%4.
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
-        const f32x4 val = {acc[rt][dt][4 * q4 + 0], acc[rt][dt][4 * q4 + 1], acc[rt][dt][4 * q4 + 2],
-                           acc[rt][dt][4 * q4 + 3]};
-        *reinterpret_cast<f32x4*>(op + dt * 32 + 8 * q4 + 4 * lg) = val;
+        const f32x16 x = acc[rt][dt];
+        const u32x2 val = {pack2<BF16>(x[4 * q4] * inv, x[4 * q4 + 1] * inv),
+                           pack2<BF16>(x[4 * q4 + 2] * inv, x[4 * q4 + 3] * inv)};
+        *reinterpret_cast<u32x2*>(op + dt * 32 + 8 * q4 + 4 * lg) = val;
       }
     }
     if (lg == 0) a.ml[prow] = make_float2(mx[rt], ltot);
   }
 }
 
-// Wave layout of a 256-row workgroup: 8 waves x 32 rows (2 waves per SIMD,
-// default) or 4 waves x 64 rows (1 wave per SIMD, K/V fragments shared by two
-// row tiles).  DSV_ATTN_WAVES=4 selects the latter.
-int wave_layout() {
-  static int w = [] {
-    const char* e = getenv("DSV_ATTN_WAVES");
-    return (e != nullptr && atoi(e) == 4) ? 4 : 8;
-  }();
-  return w;
-}
-
 template <typename T, int D, bool DMASK>
-hipError_t launch_t(const AttnArgs& a, hipStream_t s) {
+hipError_t launch_t(const AttnArgs& a, int layout, hipStream_t s) {
   const int64_t nblk = (int64_t)a.B * a.Hk * a.s_total * a.n_rb;
   if (nblk <= 0) return hipSuccess;
-  if (wave_layout() == 4)
-    hipLaunchKernelGGL((attn_splitk_kernel<T, D, 4, 64, DMASK>), dim3((unsigned)nblk), dim3(256), 0, s, a);
+  const dim3 grid((unsigned)nblk);
+  if (layout == kLayout4x64)
+    hipLaunchKernelGGL((attn_splitk_kernel<T, D, 4, 64, DMASK>), grid, dim3(256), 0, s, a);
+  else if (layout == kLayout8x32)
+    hipLaunchKernelGGL((attn_splitk_kernel<T, D, 8, 32, DMASK>), grid, dim3(512), 0, s, a);
   else
-    hipLaunchKernelGGL((attn_splitk_kernel<T, D, 8, 32, DMASK>), dim3((unsigned)nblk), dim3(512), 0, s, a);
+    hipLaunchKernelGGL((attn_splitk_kernel<T, D, 4, 32, DMASK>), grid, dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
 template <typename T, bool DMASK>
-hipError_t launch_d(const AttnArgs& a, int D, hipStream_t s) {
+hipError_t launch_d(const AttnArgs& a, int D, int layout, hipStream_t s) {
   switch (D) {
-    case 64: return launch_t<T, 64, DMASK>(a, s);
-    case 128: return launch_t<T, 128, DMASK>(a, s);
+    case 64: return launch_t<T, 64, DMASK>(a, layout, s);
+    case 128: return launch_t<T, 128, DMASK>(a, layout, s);
     default: return hipErrorInvalidValue;
   }
 }
 
 }  // namespace
 
+// Workgroup layouts (waves x rows per wave):
+//   4x32  128 rows, 2 workgroups per CU: the two workgroups on a CU are not
+//         barrier-coupled (measured slower than 8x32 at 64K keys: each
+//         K/V tile feeds half as many rows);
+//   8x32  256 rows, 1 workgroup per CU (2 waves per SIMD, one barrier;
+//         default, fastest measured);
+//   4x64  256 rows, 1 workgroup per CU (1 wave per SIMD, K/V fragments
+//         shared by two row tiles).
+// DSV_ATTN_LAYOUT=432|832|464 overrides the default (for measurements).
+int attn_layout() {
+  static int l = [] {
+    const char* e = getenv("DSV_ATTN_LAYOUT");
+    const int v = e != nullptr ? atoi(e) : 0;
+    return v == 432 ? kLayout4x32 : (v == 464 ? kLayout4x64 : kLayout8x32);
+  }();
+  return l;
+}
+
+int attn_rows_per_block() { return attn_layout() == kLayout4x32 ? 128 : 256; }
+int attn_blocks_per_cu() { return attn_layout() == kLayout4x32 ? 2 : 1; }
+
 hipError_t launch_attn(const AttnArgs& a, int dtype, int D, bool dmask, hipStream_t s) {
-  if (dtype == 0) return dmask ? launch_d<BF16, true>(a, D, s) : launch_d<BF16, false>(a, D, s);
-  return dmask ? launch_d<F16, true>(a, D, s) : launch_d<F16, false>(a, D, s);
+  const int layout = attn_layout();
+  if (dtype == 0) return dmask ? launch_d<BF16, true>(a, D, layout, s) : launch_d<BF16, false>(a, D, layout, s);
+  return dmask ? launch_d<F16, true>(a, D, layout, s) : launch_d<F16, false>(a, D, layout, s);
 }
 
 }  // namespace dsv

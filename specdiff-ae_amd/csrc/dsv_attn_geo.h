@@ -1,0 +1,102 @@
+// dsv_attn_geo.h — tile geometry and address arithmetic of the split-K
+// attention kernel, shared by the gfx950 kernel and the host-side address
+// emulation (dry-run mode of the C ABI), so the code that is bounds-checked on
+// the CPU is the code the GPU executes.
+#pragma once
+
+#include <stdint.h>
+
+#include "dsv_internal.h"
+
+namespace dsv {
+
+#define DSV_HD __host__ __device__ __forceinline__
+
+// Geometry for head_dim D.
+//   KT    keys per LDS tile
+//   CH    16-byte chunks per key row
+//   TILE  bytes of one K (or V) tile
+//   NINS  1 KiB DMA wave-instructions per K (or V) tile
+//   KPI   keys per DMA instruction
+//   RING  bytes of the LDS ring (kStages tiles of K and V); kept <= 64 KiB so
+//         every LDS-DMA destination address fits in 16 bits
+template <int D>
+struct Geo {
+  static constexpr int KT = 32;
+  static constexpr int CH = D / 8;
+  static constexpr int ROWB = 2 * D;
+  static constexpr int TILE = KT * ROWB;
+  static constexpr int NINS = TILE / 1024;
+  static constexpr int KPI = 1024 / ROWB;
+  static constexpr int STAGES = 4;
+  static constexpr int RING = STAGES * 2 * TILE;
+  static_assert(RING <= 65536, "LDS-DMA ring must stay below 64 KiB");
+};
+
+// Chunk swizzles of the LDS image (an XOR, hence its own inverse):
+//   K: chunk c of key k at slot c ^ (k & 15)         conflict-free S^T operand reads
+//   V: chunk c of key k at slot c ^ ((k & 3) << 2)   conflict-free transposed reads
+DSV_HD int k_slot(int ch, int key, int c) { return c ^ (key & ((ch < 16 ? ch : 16) - 1)); }
+DSV_HD int v_slot(int ch, int key, int c) { return c ^ (((key & 3) << 2) & (ch - 1)); }
+
+// Element offset of chunk c of logical key n of a source, for a given page id.
+DSV_HD int64_t src_elem(const KvSrc& s, bool v, int b, int kvh, int64_t n, int64_t page, int c) {
+  const int64_t sb = v ? s.v_sb : s.k_sb, sp = v ? s.v_sp : s.k_sp, sh = v ? s.v_sh : s.k_sh,
+                st = v ? s.v_st : s.k_st;
+  if (s.pt != nullptr) return b * sb + page * sp + kvh * sh + (n & ((1ll << s.ps_shift) - 1)) * st + c * 8;
+  return b * sb + n * st + kvh * sh + c * 8;
+}
+
+// How a tile's DMA is issued.
+//   kFast:  scalar base at the instruction's first key (page resolved once),
+//           per-lane offset kii*st + chunk*8, through a bounds-checked buffer
+//           resource; also used for tail tiles with per-lane keys clamped to
+//           the last valid key (an instruction's keys never straddle a page)
+//   kLane:  per-lane full address (keys clamped, page per lane); used when a
+//           page can split an instruction's keys (page < KPI or unaligned key0)
+enum DmaMode : int { kFast = 0, kLane = 1 };
+
+template <int D>
+DSV_HD int dma_mode(const KvSrc& s) {
+  if (s.pt == nullptr) return kFast;
+  return ((1ll << s.ps_shift) >= Geo<D>::KPI && (s.key0 & (Geo<D>::KPI - 1)) == 0) ? kFast : kLane;
+}
+
+// Instruction i of a tile (0..2*NINS-1: K first, then V): which half and block.
+template <int D>
+DSV_HD void dma_ins(int i, bool& is_v, int& j) {
+  is_v = i >= Geo<D>::NINS;
+  j = is_v ? i - Geo<D>::NINS : i;
+}
+
+// Fast mode.  Logical key of the instruction's scalar base and of a lane.
+//   n0 = key0 + kb + j*KPI (first key); nb = min(n0, last); nl = min(n0 + kii, last)
+DSV_HD int64_t fast_base_key(const KvSrc& s, int64_t kb, int64_t kend, int j, int kpi) {
+  const int64_t n0 = s.key0 + kb + (int64_t)j * kpi, last = s.key0 + kend - 1;
+  return n0 < last ? n0 : last;
+}
+DSV_HD int64_t fast_lane_key(const KvSrc& s, int64_t kb, int64_t kend, int j, int kpi, int kii) {
+  const int64_t n = s.key0 + kb + (int64_t)j * kpi + kii, last = s.key0 + kend - 1;
+  return n < last ? n : last;
+}
+// Per-lane element offset relative to the scalar base (key nb, chunk 0).
+DSV_HD int64_t fast_lane_elem(const KvSrc& s, bool v, int64_t nb, int64_t nl, int c) {
+  return (nl - nb) * (v ? s.v_st : s.k_st) + c * 8;
+}
+
+// Buffer-resource range: bytes from the scalar base to the end of the source
+// (accesses at or beyond it read zeros instead of faulting).
+DSV_HD uint32_t rsrc_range(int64_t span_bytes, int64_t base_elem) {
+  const int64_t r = span_bytes - 2 * base_elem;
+  return r <= 0 ? 0u : (r >= 0xffffffffll ? 0xffffffffu : (uint32_t)r);
+}
+
+// Lane mode: logical key of a lane (clamped to the last valid key).
+DSV_HD int64_t lane_key(const KvSrc& s, int64_t kb, int64_t kend, int key_in_tile) {
+  const int64_t n = s.key0 + kb + key_in_tile, last = s.key0 + kend - 1;
+  return n < last ? n : last;
+}
+
+DSV_HD int64_t clamp_page(int64_t pg, int64_t n_phys) { return pg < 0 ? 0 : (pg >= n_phys ? n_phys - 1 : pg); }
+
+}  // namespace dsv

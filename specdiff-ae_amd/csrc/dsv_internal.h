@@ -43,6 +43,8 @@ struct KvSrc {
   int64_t pt_sb;       // page-table batch stride (0 -> shared by all batches)
   int64_t key0;        // logical index of this source's key 0
   int64_t n_phys;      // physical pages in the pool (page ids are clamped to it)
+  int64_t k_bytes;     // byte span of the K (V) tensor view from its base pointer
+  int64_t v_bytes;
 };
 
 // Arguments of the split-K attention kernel (kernels 1 and 2).
@@ -74,14 +76,14 @@ struct AttnArgs {
 
   const int32_t* row_perm; // [M] node packing order (nullptr -> identity)
 
-  float* opart;            // [S, B, Hk, R, D] unnormalised partial outputs
+  uint16_t* opart;         // [S, B, Hk, R, D] bf16 partial outputs, normalised per split
   float2* ml;              // [S, B, Hk, R] (running max in log2 units, sum)
   int s_total;             // n_splits + has_tree
 };
 
 // Arguments of the LSE merge kernel (kernel 3).
 struct MergeArgs {
-  const float* opart;
+  const uint16_t* opart;   // bf16, normalised per split
   const float2* ml;
   int s_total;
   int B, M, H, Hk, G, R, D;
@@ -125,6 +127,11 @@ struct AcceptArgs {
 // Launchers (defined in the .hip files, called by the C-ABI layer).
 // ---------------------------------------------------------------------------
 hipError_t launch_attn(const AttnArgs& a, int dtype, int D, bool dmask, hipStream_t s);
+// Workgroup layout of the attention kernel and what the host plan needs from it.
+enum AttnLayout : int { kLayout4x32 = 0, kLayout8x32 = 1, kLayout4x64 = 2 };
+int attn_layout();
+int attn_rows_per_block();
+int attn_blocks_per_cu();
 hipError_t launch_merge(const MergeArgs& a, hipStream_t s);
 hipError_t launch_accept(const AcceptArgs& a, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1);
 

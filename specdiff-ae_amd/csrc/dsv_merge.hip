@@ -1,10 +1,13 @@
 // dsv_merge.hip — kernel 3: log-sum-exp merge of split-K partials on gfx950.
 //
-// One wave64 per output row (batch, KV head, packed row).  Lane s holds the
-// statistics (m_s, l_s) of split s; the wave computes M* = max_s m_s and
-// L = sum_s 2^(m_s - M*) l_s with cross-lane reductions, turns each split
-// into a coefficient c_s = 2^(m_s - M*) / L, then streams the partial rows
-// (coalesced 256-byte reads per split) and accumulates O = sum_s c_s O_s.
+// One wave64 per output row (batch, KV head, packed row).  Split s left a
+// normalised bf16 row O_s and (m_s, l_s) = (running max in log2 units, sum of
+// exponentials relative to it).  With M* = max_s m_s and
+// w_s = l_s * 2^(m_s - M*), the merged row is O = sum_s w_s O_s / sum_s w_s and
+// LSE = ln2 * (M* + log2 sum_s w_s).
+// Lanes are split into (split group, 16-byte column chunk): every lane keeps
+// several independent 16-byte loads in flight, then the split groups are
+// reduced across lanes with DPP-class shuffles.
 // This is the S-way generalisation of the reference's 2-way combine
 // out = O_tree*(1-w) + O_prefix*w with w = sigmoid(lse_prefix - lse_tree)
 // (runtime/tree_attention.py:535-539, llama_target_model.py:862-866), done in
@@ -32,6 +35,9 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
 __device__ __forceinline__ void store_val(void* base, int dtype, int64_t off, float x) {
   if (dtype == 2) {
     reinterpret_cast<float*>(base)[off] = x;
@@ -42,66 +48,63 @@ __device__ __forceinline__ void store_val(void* base, int dtype, int64_t off, fl
   }
 }
 
+template <int D>
 __global__ void __launch_bounds__(256) lse_merge_kernel(const MergeArgs a) {
+  constexpr int TPR = D / 8;        // 16-byte column chunks per row
+  constexpr int SG = 64 / TPR;      // split groups per wave
   const int lane = threadIdx.x & 63;
+  const int tc = lane % TPR, sg = lane / TPR;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int64_t nrows = (int64_t)a.B * a.Hk * a.R;
   if (row >= nrows) return;
   const int r = (int)(row % a.R);
   const int kvh = (int)((row / a.R) % a.Hk);
   const int b = (int)(row / ((int64_t)a.R * a.Hk));
-  const int64_t split_stride = nrows;  // rows per split
 
-  // Pass 1: global max over splits.
+  // Global max and total weight over splits.
   float mloc = kNegInf;
-  for (int s = lane; s < a.s_total; s += 64) mloc = fmaxf(mloc, a.ml[s * split_stride + row].x);
+  for (int s = lane; s < a.s_total; s += 64) mloc = fmaxf(mloc, a.ml[s * nrows + row].x);
   const float mstar = wave_max(mloc);
-
-  // Pass 2: total weight.
   float lloc = 0.f;
   if (mstar != kNegInf) {
     for (int s = lane; s < a.s_total; s += 64) {
-      const float2 st = a.ml[s * split_stride + row];
+      const float2 st = a.ml[s * nrows + row];
       if (st.x != kNegInf) lloc += __builtin_amdgcn_exp2f(st.x - mstar) * st.y;
     }
   }
   const float L = wave_sum(lloc);
   const float invL = L > 0.f ? 1.f / L : 0.f;
 
-  // Pass 3: weighted sum of partial rows; coefficients broadcast per split.
-  constexpr int kMaxPer = 4;  // D <= 256
-  float acc[kMaxPer];
+  float acc[8];
 #pragma unroll
-  for (int i = 0; i < kMaxPer; ++i) acc[i] = 0.f;
-  for (int s0 = 0; s0 < a.s_total; s0 += 64) {
-    float c = 0.f;
-    const int s = s0 + lane;
-    if (s < a.s_total && mstar != kNegInf) {
-      const float mx = a.ml[s * split_stride + row].x;
-      if (mx != kNegInf) c = __builtin_amdgcn_exp2f(mx - mstar) * invL;
-    }
-    const int n = min(64, a.s_total - s0);
-    for (int j = 0; j < n; ++j) {
-      const float cj = __shfl(c, j);
-      if (cj == 0.f) continue;
-      const float* op = a.opart + ((int64_t)(s0 + j) * split_stride + row) * a.D;
+  for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+  if (mstar != kNegInf) {
+#pragma unroll 4
+    for (int s = sg; s < a.s_total; s += SG) {
+      const float2 st = a.ml[s * nrows + row];
+      const float w = (st.x == kNegInf) ? 0.f : __builtin_amdgcn_exp2f(st.x - mstar) * st.y;
+      const u32x4 raw = *reinterpret_cast<const u32x4*>(a.opart + (s * nrows + row) * D + tc * 8);
 #pragma unroll
-      for (int i = 0; i < kMaxPer; ++i) {
-        const int d = lane + 64 * i;
-        if (d < a.D) acc[i] = fmaf(cj, op[d], acc[i]);
+      for (int e = 0; e < 4; ++e) {
+        acc[2 * e] = fmaf(w, bf16_lo(raw[e]), acc[2 * e]);
+        acc[2 * e + 1] = fmaf(w, bf16_hi(raw[e]), acc[2 * e + 1]);
       }
     }
+  }
+#pragma unroll
+  for (int o = TPR; o < 64; o <<= 1) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] += __shfl_xor(acc[e], o);
   }
 
   const int g = r / a.M;
   const int mi = r - g * a.M;
   const int m = a.row_perm ? min(max(a.row_perm[mi], 0), a.M - 1) : mi;
   const int h = kvh * a.G + g;
-  const int64_t obase = (int64_t)b * a.o_sb + (int64_t)m * a.o_sm + (int64_t)h * a.o_sh;
+  if (sg == 0) {
+    const int64_t obase = (int64_t)b * a.o_sb + (int64_t)m * a.o_sm + (int64_t)h * a.o_sh + tc * 8;
 #pragma unroll
-  for (int i = 0; i < kMaxPer; ++i) {
-    const int d = lane + 64 * i;
-    if (d < a.D) store_val(a.out, a.out_dtype, obase + d, acc[i]);
+    for (int e = 0; e < 8; ++e) store_val(a.out, a.out_dtype, obase + e, acc[e] * invL);
   }
   if (lane == 0) {
     const float lse = (L > 0.f) ? (mstar + __log2f(L)) * kLn2 : kNegInf;
@@ -119,7 +122,13 @@ __global__ void __launch_bounds__(256) lse_merge_kernel(const MergeArgs a) {
 hipError_t launch_merge(const MergeArgs& a, hipStream_t s) {
   const int64_t nrows = (int64_t)a.B * a.Hk * a.R;
   if (nrows <= 0) return hipSuccess;
-  hipLaunchKernelGGL(lse_merge_kernel, dim3((unsigned)((nrows + 3) / 4)), dim3(256), 0, s, a);
+  const dim3 grid((unsigned)((nrows + 3) / 4));
+  if (a.D == 128)
+    hipLaunchKernelGGL(lse_merge_kernel<128>, grid, dim3(256), 0, s, a);
+  else if (a.D == 64)
+    hipLaunchKernelGGL(lse_merge_kernel<64>, grid, dim3(256), 0, s, a);
+  else
+    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 

@@ -55,6 +55,8 @@ SIGNATURES = {
     "dsv_version": (ctypes.c_int, []),
     "dsv_last_error": (ctypes.c_char_p, []),
     "dsv_set_timing_events": (ctypes.c_int, [_V, _V]),
+    "dsv_set_dry_run": (ctypes.c_int, [ctypes.c_int]),
+    "dsv_dry_run_checks": (_I64, []),
     "dsv_attn_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_int]),
     "dsv_prefix_attention_forward": (ctypes.c_int, [_P, _P, _P, _I64, _P, _P, _V, _SZ, _V]),
     "dsv_tree_attention_forward": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _V, _SZ, _V]),

@@ -25,7 +25,8 @@ def run_and_compare(logits, draft, parent_ref, pos, max_depth, mode="greedy", **
         if mode == "greedy":
             w_toks, w_ids, w_alen, w_next, w_id = oacc.greedy_walk(*args)
         else:
-            w_toks, w_ids, w_alen, w_next, w_id = oacc.typical_walk(*args, **kw)
+            w_toks, w_ids, w_alen, w_next, w_id = oacc.typical_walk(
+                *args, temperature=kw["temperature"], eps=kw["posterior_threshold"], alpha=kw["posterior_alpha"])
         L = len(w_ids)
         assert info[t].tolist() == [w_id, w_alen, w_next, L], f"tree {t}"
         assert path[t, :L].tolist() == w_ids and (path[t, L:] == -1).all()
