@@ -3,6 +3,7 @@
 // interface each entry point replaces are in include/dsv.h.
 
 #include "dsv.h"
+#include "dsv_attn_geo.h"
 #include "dsv_check.h"
 #include "dsv_internal.h"
 
@@ -290,8 +291,11 @@ AttnExtents common_extents(const dsv_tensor* q, const dsv_tensor* out, void* ws,
   return ex;
 }
 
-int run(const AttnArgs& a, const MergeArgs& m, int dtype, int D, bool dmask, hipStream_t st,
+int run(const AttnArgs& a_in, const MergeArgs& m, int dtype, int D, bool dmask, hipStream_t st,
         const AttnExtents& ex) {
+  AttnArgs a = a_in;
+  a.pre.fast32 = dsv::fast32_ok(a.pre, a.pre.key0 + a.n_pre) ? 1 : 0;
+  a.tree.fast32 = a.has_tree && dsv::fast32_ok(a.tree, a.tree.key0 + a.M) ? 1 : 0;
   if (g_dry_run) {
     std::string err;
     int64_t n = 0;

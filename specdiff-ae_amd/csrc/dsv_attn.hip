@@ -13,15 +13,15 @@
 //
 // Data movement per 32-key tile: K and V rows go HBM -> LDS by LDS-DMA
 // (buffer_load_dwordx4 ... lds), one 1 KiB wave-instruction per 4 keys, into
-// a 4-stage LDS ring (three tiles in flight while one is consumed; the ring
-// stays below 64 KiB).  Each lane's global chunk is chosen so that the LDS
+// a 4-stage LDS ring (two tiles being consumed, two in flight; the ring stays
+// below 64 KiB).  Each lane's global chunk is chosen so that the LDS
 // image is XOR-swizzled for conflict-free operand reads.  The fast path
 // resolves the page once per instruction into a scalar base wrapped in a
 // buffer resource whose range ends at the tensor's end, so the hardware
 // bounds-checks every lane.  Address arithmetic lives in dsv_attn_geo.h and
 // is shared with the host-side emulation used by the dry-run mode.
 //
-// Math per tile, per wave of WR rows (WR = 32 or 64):
+// Math per tile, per wave of 32 rows:
 //   S^T[key, row] = K[key, :] . Q[row, :]      v_mfma_f32_32x32x16_{bf16,f16}
 //   P = exp2(S * log2(e)/sqrt(D) - m_row)      online softmax, lazy rescale
 //   O^T[d, row]  += V^T[d, key] . P^T[key,row] v_mfma_f32_32x32x16_{bf16,f16}
@@ -83,7 +83,7 @@ __device__ __forceinline__ uint32_t pack2<F16>(float lo, float hi) {
 // Combine a value with the one held by lane (lane ^ 32).
 __device__ __forceinline__ float xor32_max(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return __builtin_elementwise_maximum(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float xor32_sum(float x) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
@@ -109,6 +109,21 @@ __device__ __forceinline__ void dma_buf(uint32_t lds, const void* base, uint32_t
   r[1] = __builtin_amdgcn_readfirstlane((int)(uint32_t)(p >> 32));
   r[2] = __builtin_amdgcn_readfirstlane((int)range);
   r[3] = 0x00020000;
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(voff), "s"(r)
+               : "memory", "m0");
+}
+// A buffer resource (base, byte range) in SGPRs, built once and reused.
+__device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t range) {
+  const uint64_t p = (uint64_t)base;
+  i32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)p);
+  r[1] = __builtin_amdgcn_readfirstlane((int)(uint32_t)(p >> 32));
+  r[2] = __builtin_amdgcn_readfirstlane((int)range);
+  r[3] = 0x00020000;
+  return r;
+}
+__device__ __forceinline__ void dma_rs(uint32_t lds, i32x4 r, uint32_t voff) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(voff), "s"(r)
                : "memory", "m0");
@@ -146,19 +161,42 @@ __device__ __forceinline__ bool tmask_keep(const AttnArgs& a, int b, int i, int 
   }
 }
 
-// Waves per SIMD: two for 32-row waves (8x32 layout, or two 4x32 workgroups
-// per CU), one for 64-row waves.
-template <typename T, int D, int NW, int WR, bool DMASK>
-__global__ void __launch_bounds__(NW * 64, WR == 32 ? 2 : 1) attn_splitk_kernel(const AttnArgs a) {
+// A compile-time integer: the ring stage of an unrolled loop step, so that
+// every LDS address of the stage folds into an instruction offset.
+template <int N>
+struct IC {
+  static constexpr int value = N;
+};
+
+// Row maximum of a lane's 16 scores (NaN-propagating, like torch.max;
+// v_maximum3_f32 on gfx950).
+__device__ __forceinline__ float max16(const f32x16& s) {
+  float m = __builtin_elementwise_maximum(s[0], s[1]);
+#pragma unroll
+  for (int v = 2; v < 16; ++v) m = __builtin_elementwise_maximum(m, s[v]);
+  return m;
+}
+
+// One workgroup = 8 waves x 32 query rows (two waves per SIMD).
+//
+// Software pipeline per wave: iteration t owns the scores S(t), already
+// computed.  It waits for tile t+1 (two tiles stay in flight), then runs
+// the softmax of S(t) on the VALU while the MFMA pipe computes S(t+1) from
+// tile t+1's K, and finally O += V(t)^T P(t)^T.  Ring stage of tile t: t & 3;
+// tile t+3 goes into stage (t+3) & 3, whose previous tile (t-1) every wave has
+// finished with once the barrier of iteration t is passed.
+template <typename T, int D, bool DMASK>
+__global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
   using G = Geo<D>;
+  constexpr int NW = 8;
   constexpr int NT = NW * 64;
   constexpr int KT = G::KT;
   constexpr int KS = D / 16;                   // k-steps of the Q.K^T product
   constexpr int DT = D / 32;                   // 32-row d tiles of the P.V product
   constexpr int CH = G::CH;
-  constexpr int RT = WR / 32;                  // 32-row MFMA tiles per wave
   constexpr int IPW = 2 * G::NINS / NW;        // DMA instructions per wave per tile
   static_assert(IPW * NW == 2 * G::NINS, "tile DMA must split evenly over waves");
+  static_assert(G::STAGES == 4, "the loop is unrolled over a 4-stage ring");
   constexpr int PT_OFF = G::RING;
   constexpr int VIS_OFF = PT_OFF + kPageLds * 4;
   constexpr int LDS_BYTES = VIS_OFF + kTreeMaxM * kTreeMaxW * 8;
@@ -197,6 +235,7 @@ __global__ void __launch_bounds__(NW * 64, WR == 32 ? 2 : 1) attn_splitk_kernel(
   }
   const int64_t nkeys = kend - kstart;
   const int ntiles = nkeys > 0 ? (int)((nkeys + KT - 1) / KT) : 0;
+  const int nfull = nkeys > 0 ? (int)(nkeys / KT) : 0;  // tiles without tail keys
   const bool paged = src.pt != nullptr;
   const int mode = dma_mode<D>(src);
 
@@ -242,29 +281,68 @@ __global__ void __launch_bounds__(NW * 64, WR == 32 ? 2 : 1) attn_splitk_kernel(
   // ---- DMA issue of one tile into its ring stage ------------------------------
   // Instruction i covers keys [j*KPI, (j+1)*KPI) of the tile's K or V; lane p
   // fills LDS bytes [16p, 16p+16) of that KiB = key j*KPI + p/CH, slot p%CH,
-  // which holds global chunk slot ^ swizzle(key).
+  // which holds global chunk slot ^ swizzle(key).  In a full tile the lane's
+  // byte offset from the instruction's base key does not change from tile to
+  // tile: it is computed once.
   const int kii = lane / CH;
   const int slot = lane % CH;
-  auto issue_tile = [&](int t) {
-    const int stage = t & (G::STAGES - 1);
+  uint32_t voff_full[IPW];
+#pragma unroll
+  for (int x = 0; x < IPW; ++x) {
+    bool is_v;
+    int j;
+    dma_ins<D>(wid * IPW + x, is_v, j);
+    const int key_t = j * G::KPI + kii;
+    const int c = is_v ? v_slot(CH, key_t, slot) : k_slot(CH, key_t, slot);
+    voff_full[x] = (uint32_t)(fast_lane_elem(src, is_v, 0, kii, c) * 2);
+  }
+  // kFast32: this workgroup's K and V buffer resources, built once.
+  i32x4 rs_kv[2] = {i32x4{0, 0, 0, 0}, i32x4{0, 0, 0, 0}};
+  if (mode == kFast32) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int64_t wb = wg_base_elem(src, h == 1, b, kvh);
+      rs_kv[h] = make_rsrc((h == 1 ? src.v : src.k) + wb, rsrc_range(h == 1 ? src.v_bytes : src.k_bytes, wb));
+    }
+  }
+  auto issue_tile = [&](auto stage_c, int t) {
+    constexpr int stage = decltype(stage_c)::value;
     const int64_t kb = kstart + (int64_t)t * KT;
+    const bool full = t < nfull;
 #pragma unroll
     for (int x = 0; x < IPW; ++x) {
       bool is_v;
       int j;
       dma_ins<D>(wid * IPW + x, is_v, j);
       const int key_t = j * G::KPI + kii;  // key within the tile
-      const int c = is_v ? v_slot(CH, key_t, slot) : k_slot(CH, key_t, slot);
       const uint32_t dst = lds_addr(smem + (stage * 2 + (is_v ? 1 : 0)) * G::TILE + j * 1024);
       const uint16_t* base = is_v ? src.v : src.k;
-      if (mode == kFast) {
+      if (mode == kFast32) {
+        // Keys fit in 31 bits in this mode: per-tile arithmetic is 32-bit scalar.
+        const int kb32 = (int)(src.key0 + kb);
+        uint32_t nb = (uint32_t)(kb32 + j * G::KPI);
+        uint32_t vo = voff_full[x];
+        if (!full) {
+          const int64_t nb64 = fast_base_key(src, kb, kend, j, G::KPI);
+          const int c = is_v ? v_slot(CH, key_t, slot) : k_slot(CH, key_t, slot);
+          vo = (uint32_t)(fast_lane_elem(src, is_v, nb64, fast_lane_key(src, kb, kend, j, G::KPI, kii), c) * 2);
+          nb = (uint32_t)nb64;
+        }
+        const uint32_t page =
+            paged ? (uint32_t)__builtin_amdgcn_readfirstlane(pt_lds[(int)(nb >> src.ps_shift) - (int)pt_lo]) : 0u;
+        dma_rs(dst, rs_kv[is_v ? 1 : 0], vo + tile_off32(src, is_v, nb, page));
+      } else if (mode == kFast) {
         const int64_t nb = fast_base_key(src, kb, kend, j, G::KPI);
-        const int64_t nl = fast_lane_key(src, kb, kend, j, G::KPI, kii);
         const int64_t page = paged ? __builtin_amdgcn_readfirstlane(pt_lds[(nb >> src.ps_shift) - pt_lo]) : 0;
         const int64_t be = src_elem(src, is_v, b, kvh, nb, page, 0);
-        const int64_t le = fast_lane_elem(src, is_v, nb, nl, c);
-        dma_buf(dst, base + be, rsrc_range(is_v ? src.v_bytes : src.k_bytes, be), (uint32_t)(le * 2));
+        uint32_t vo = voff_full[x];
+        if (!full) {
+          const int c = is_v ? v_slot(CH, key_t, slot) : k_slot(CH, key_t, slot);
+          vo = (uint32_t)(fast_lane_elem(src, is_v, nb, fast_lane_key(src, kb, kend, j, G::KPI, kii), c) * 2);
+        }
+        dma_buf(dst, base + be, rsrc_range(is_v ? src.v_bytes : src.k_bytes, be), vo);
       } else {
+        const int c = is_v ? v_slot(CH, key_t, slot) : k_slot(CH, key_t, slot);
         const int64_t n = lane_key(src, kb, kend, key_t);
         const int64_t page = paged ? pt_lds[(n >> src.ps_shift) - pt_lo] : 0;
         dma_lane(dst, base + src_elem(src, is_v, b, kvh, n, page, c));
@@ -274,272 +352,246 @@ __global__ void __launch_bounds__(NW * 64, WR == 32 ? 2 : 1) attn_splitk_kernel(
 
   // ---- this wave's query rows: Q fragments (B operand of S^T = K.Q^T) --------
   // lane (row lj, group lg) holds Q[row, 16*ks + 8*lg .. +8].
-  const int row0 = rb * (NW * WR) + wid * WR;
+  const int row0 = rb * (NW * 32) + wid * 32;
   const bool wave_active = row0 < a.R;
-  u32x4 qf[RT][KS];
-  int node_of[RT];
-  bool rvalid[RT];
+  const int r_me = row0 + lj;
+  const bool rvalid = r_me < a.R;
+  u32x4 qf[KS];
+  int node_of = 0;
+  if (rvalid) {
+    const int g = r_me / a.M;
+    const int mi = r_me - g * a.M;
+    // A permutation entry outside [0, M) is clamped: no access leaves q.
+    const int m = a.row_perm ? min(max(a.row_perm[mi], 0), a.M - 1) : mi;
+    node_of = m;
+    const uint16_t* qp = a.q + b * a.q_sb + (int64_t)m * a.q_sm + (int64_t)(kvh * a.G + g) * a.q_sh + lg * 8;
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    const int r = row0 + rt * 32 + lj;
-    rvalid[rt] = r < a.R;
-    node_of[rt] = 0;
-    if (rvalid[rt]) {
-      const int g = r / a.M;
-      const int mi = r - g * a.M;
-      // A permutation entry outside [0, M) is clamped: no access leaves q.
-      const int m = a.row_perm ? min(max(a.row_perm[mi], 0), a.M - 1) : mi;
-      node_of[rt] = m;
-      const uint16_t* qp = a.q + b * a.q_sb + (int64_t)m * a.q_sm + (int64_t)(kvh * a.G + g) * a.q_sh + lg * 8;
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = ld16(qp + ks * 16);
+  } else {
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) qf[rt][ks] = ld16(qp + ks * 16);
-    } else {
+    for (int ks = 0; ks < KS; ++ks) qf[ks] = u32x4{0, 0, 0, 0};
+  }
+
+  f32x16 acc[DT];
+  float mx = kNegInf, lsum = 0.f;
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) qf[rt][ks] = u32x4{0, 0, 0, 0};
+  for (int dt = 0; dt < DT; ++dt) acc[dt] = f32x16{};
+
+  // Per-lane LDS byte offsets of the operand reads within a tile (the stage
+  // part is a compile-time offset).
+  //   K (A operand of S^T): key lj, chunk 2*ks + lg.
+  //   V^T (two transposed reads per d tile): 16-lane block bl = lane/16 holds
+  //   d rows [16*(bl&1), +16) of a 32-row d tile and key group g = bl>>1;
+  //   lane i of the block addresses key row 16*hh + 4*g + i/4 (+8 for the
+  //   second read), columns d0 + 4*(i%4) .. +3.
+  uint32_t koff[KS], voff[DT];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) koff[ks] = lj * (2 * D) + k_slot(CH, lj, 2 * ks + lg) * 16;
+  {
+    const int bl = lane >> 4, bi = lane & 15;
+    const int vkey = 4 * (bl >> 1) + (bi >> 2);
+    const int vcol = 16 * (bl & 1) + 4 * (bi & 3);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const int col = dt * 32 + vcol;
+      // (vkey + 16*hh + 8*e) & 3 == vkey & 3: the swizzle is the same for all
+      // four reads of a d tile.
+      voff[dt] = vkey * (2 * D) + v_slot(CH, vkey, col >> 3) * 16 + (col & 7) * 2;
     }
   }
 
-  f32x16 acc[RT][DT];
-  float mx[RT], lsum[RT];
+  // S^T tile of `stage` (32 keys x this wave's 32 rows).
+  auto qk = [&](auto stage_c) {
+    constexpr int stage = decltype(stage_c)::value;
+    const uint8_t* kt = smem + stage * 2 * G::TILE;
+    f32x16 s = f32x16{};
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    mx[rt] = kNegInf;
-    lsum[rt] = 0.f;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) acc[rt][dt] = f32x16{};
-  }
-
-  // Per-lane constant parts of the V^T operand reads (two transposed reads):
-  // 16-lane block bl = lane/16 holds d rows [16*(bl&1), +16) of a 32-row d
-  // tile and key group g = bl>>1; lane i of the block addresses key row
-  // 16*hh + 4*g + i/4 (+8 for the second read), columns d0 + 4*(i%4) .. +3.
-  const int bl = lane >> 4, bi = lane & 15;
-  const int vkey = 4 * (bl >> 1) + (bi >> 2);
-  const int vcol = 16 * (bl & 1) + 4 * (bi & 3);
-
-  // ---- one tile of compute ---------------------------------------------------
-  auto compute = [&](const uint8_t* kt_lds, const uint8_t* vt_lds, int64_t kb, bool masked, int t) {
-    // ---- S^T = K . Q^T --------------------------------------------------------
-    f32x16 st[RT];
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) st[rt] = f32x16{};
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const u32x4 kf = *reinterpret_cast<const u32x4*>(kt_lds + lj * (2 * D) + k_slot(CH, lj, 2 * ks + lg) * 16);
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt) st[rt] = mfma32<T>(kf, qf[rt][ks], st[rt]);
-    }
-
-    // ---- masking (tail tiles, tree split, byte masks) -------------------------
-    // 16-bit keep mask per lane: bit v <-> key 4*lg + 8*(v/4) + v%4 of the tile.
-    if (masked) {
-      const int lim = (int)min(kend - kb, (int64_t)KT) - 4 * lg;  // valid keys from 4*lg
-      uint32_t tail = 0;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int c = min(max(lim - 8 * q, 0), 4);  // valid keys among 8q .. 8q+3
-        tail |= ((1u << c) - 1u) << (4 * q);
-      }
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        uint32_t keep = tail;
-        if (is_tree) {
-          // Visibility bits of this tile's keys, shifted to this lane's keys.
-          const uint64_t vw = rvalid[rt] ? vis_lds[node_of[rt] * kTreeMaxW + (t >> 1)] : 0ull;
-          const uint32_t vb = (uint32_t)(vw >> ((t & 1) * 32 + 4 * lg));
-          keep &= (vb & 0xFu) | ((vb >> 4) & 0xF0u) | ((vb >> 8) & 0xF00u) | ((vb >> 12) & 0xF000u);
-        }
-        if constexpr (DMASK) {
-          const uint8_t* mrow = a.dmask + (int64_t)b * a.dm_sb + (int64_t)node_of[rt] * a.dm_sm;
-          const int64_t n0 = kb + 4 * lg;
-          uint32_t mb = 0;
-#pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int64_t n = n0 + 8 * (v >> 2) + (v & 3);
-            mb |= (uint32_t)((n < a.dm_n) && (mrow[n * a.dm_sn] != 0)) << v;
-          }
-          keep &= rvalid[rt] ? mb : 0u;
-        }
-#pragma unroll
-        for (int v = 0; v < 16; ++v) st[rt][v] = ((keep >> v) & 1u) ? st[rt][v] : kNegInf;
-      }
-    }
-
-    // ---- online softmax (log2 domain, lazy rescale) ---------------------------
-    float mt[RT];
-    bool need = false;
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-      float m0 = fmaxf(st[rt][0], st[rt][1]);
-#pragma unroll
-      for (int v = 2; v < 16; v += 2) m0 = fmaxf(m0, fmaxf(st[rt][v], st[rt][v + 1]));
-      mt[rt] = xor32_max(m0) * a.scale_log2;
-      need = need || (mt[rt] > mx[rt] + kRescaleTau);
-    }
-    if (__ballot(need) != 0ull) {
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt) {
-        const float mn = fmaxf(mx[rt], mt[rt]);
-        const float al = (mn == mx[rt]) ? 1.f : __builtin_amdgcn_exp2f(mx[rt] - mn);
-        mx[rt] = mn;
-        lsum[rt] *= al;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) acc[rt][dt] *= al;
-      }
-    }
-
-    u32x4 pk[RT][2];
-#pragma unroll
-    for (int rt = 0; rt < RT; ++rt) {
-      const float ms = (mx[rt] == kNegInf) ? 0.f : mx[rt];
-      float ls = lsum[rt];
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        uint32_t w4[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float p0 = __builtin_amdgcn_exp2f(fmaf(st[rt][hh * 8 + 2 * e], a.scale_log2, -ms));
-          const float p1 = __builtin_amdgcn_exp2f(fmaf(st[rt][hh * 8 + 2 * e + 1], a.scale_log2, -ms));
-          w4[e] = pack2<T>(p0, p1);
-          // The normaliser sums the unrounded probabilities: the LSE is an
-          // output in its own right and keeps fp32 accuracy.
-          ls += p0 + p1;
-        }
-        pk[rt][hh] = u32x4{w4[0], w4[1], w4[2], w4[3]};
-      }
-      lsum[rt] = ls;
-    }
-
-    // ---- O^T += V^T . P^T -----------------------------------------------------
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      const int k0 = hh * 16 + vkey;  // first read: keys k0; second: k0 + 8
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const int col = dt * 32 + vcol;
-        const int c = col >> 3, cw = (col & 7) * 2;
-        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_s16x4*)(vt_lds + k0 * (2 * D) + v_slot(CH, k0, c) * 16 + cw));
-        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_s16x4*)(vt_lds + (k0 + 8) * (2 * D) + v_slot(CH, k0 + 8, c) * 16 + cw));
-        const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
-        const u32x4 vf = {l2[0], l2[1], h2[0], h2[1]};
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt) acc[rt][dt] = mfma32<T>(vf, pk[rt][hh], acc[rt][dt]);
-      }
-    }
+    for (int ks = 0; ks < KS; ++ks)
+      s = mfma32<T>(*reinterpret_cast<const u32x4*>(kt + koff[ks]), qf[ks], s);
+    return s;
   };
 
-  // ---- main loop over tiles: 4-stage DMA ring, one barrier per tile -----------
-  for (int t = 0; t < 3 && t < ntiles; ++t) issue_tile(t);
-  for (int t = 0; t < ntiles; ++t) {
-    // Tile t's loads are the oldest outstanding ones of this wave; the
-    // (up to two) newer issued tiles may stay in flight.
-    const int newer = min(ntiles - 1 - t, 2);
-    if (newer >= 2)
+  // Keep mask of the scores of tile t (tail keys, tree visibility, byte mask).
+  // Bit v of a lane <-> key 4*lg + 8*(v/4) + v%4 of the tile.
+  auto mask_scores = [&](f32x16& s, int t) {
+    const int64_t kb = kstart + (int64_t)t * KT;
+    const int lim = (int)min(kend - kb, (int64_t)KT) - 4 * lg;  // valid keys from 4*lg
+    uint32_t keep = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int c = min(max(lim - 8 * q, 0), 4);  // valid keys among 8q .. 8q+3
+      keep |= ((1u << c) - 1u) << (4 * q);
+    }
+    if (is_tree) {
+      // Visibility bits of this tile's keys, shifted to this lane's keys.
+      const uint64_t vw = rvalid ? vis_lds[node_of * kTreeMaxW + (t >> 1)] : 0ull;
+      const uint32_t vb = (uint32_t)(vw >> ((t & 1) * 32 + 4 * lg));
+      keep &= (vb & 0xFu) | ((vb >> 4) & 0xF0u) | ((vb >> 8) & 0xF00u) | ((vb >> 12) & 0xF000u);
+    }
+    if constexpr (DMASK) {
+      const uint8_t* mrow = a.dmask + (int64_t)b * a.dm_sb + (int64_t)node_of * a.dm_sm;
+      const int64_t n0 = kb + 4 * lg;
+      uint32_t mb = 0;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t n = n0 + 8 * (v >> 2) + (v & 3);
+        mb |= (uint32_t)((n < a.dm_n) && (mrow[n * a.dm_sn] != 0)) << v;
+      }
+      keep &= rvalid ? mb : 0u;
+    }
+#pragma unroll
+    for (int v = 0; v < 16; ++v) s[v] = ((keep >> v) & 1u) ? s[v] : kNegInf;
+  };
+
+  // One pipelined step: tile t in ring stage S (t & 3 == S).
+  f32x16 s_cur = f32x16{};
+  auto step = [&](auto stage_c, int t) {
+    constexpr int S = decltype(stage_c)::value;
+    // Tile t+1 landed for every wave; every wave finished tile t-1.
+    if (t + 1 < ntiles) {
+      if (t + 2 < ntiles)
+        wait_vmcnt<IPW>();
+      else
+        wait_vmcnt<0>();
+    }
+    barrier_lds();
+    if (t + 3 < ntiles) issue_tile(IC<(S + 3) & 3>{}, t + 3);
+    if (!wave_active) return;
+
+    // V^T fragments of tile t.
+    const uint8_t* vt = smem + (S * 2 + 1) * G::TILE;
+    u32x4 vf[2][DT];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const uint8_t* p = vt + voff[dt] + hh * 16 * (2 * D);
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p);
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p + 8 * (2 * D)));
+        const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+        vf[hh][dt] = u32x4{l2[0], l2[1], h2[0], h2[1]};
+      }
+
+    if (is_tree || DMASK || t >= nfull) mask_scores(s_cur, t);
+
+    // Online softmax of S(t) (log2 domain, lazy rescale).
+    const float mt = xor32_max(max16(s_cur)) * a.scale_log2;
+    if (__ballot(mt > mx + kRescaleTau) != 0ull) {
+      const float mn = __builtin_elementwise_maximum(mx, mt);
+      const float al = (mn == mx) ? 1.f : __builtin_amdgcn_exp2f(mx - mn);
+      mx = mn;
+      lsum *= al;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) acc[dt] *= al;
+    }
+
+    // S(t+1) on the MFMA pipe (tile t+1 is in stage S+1; past the last tile
+    // the product reads a stale stage and is discarded).
+    const f32x16 s_next = qk(IC<(S + 1) & 3>{});
+
+    const float ms = (mx == kNegInf) ? 0.f : mx;
+    u32x4 pk[2];
+    float ls = lsum;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      uint32_t w4[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(s_cur[hh * 8 + 2 * e], a.scale_log2, -ms));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(s_cur[hh * 8 + 2 * e + 1], a.scale_log2, -ms));
+        w4[e] = pack2<T>(p0, p1);
+        // The normaliser sums the unrounded probabilities: the LSE is an
+        // output in its own right and keeps fp32 accuracy.
+        ls += p0 + p1;
+      }
+      pk[hh] = u32x4{w4[0], w4[1], w4[2], w4[3]};
+    }
+    lsum = ls;
+
+    // O^T += V^T . P^T
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) acc[dt] = mfma32<T>(vf[hh][dt], pk[hh], acc[dt]);
+    s_cur = s_next;
+  };
+
+  // ---- main loop: prologue, then steps unrolled over the 4 ring stages --------
+  if (ntiles > 0) issue_tile(IC<0>{}, 0);
+  if (ntiles > 1) issue_tile(IC<1>{}, 1);
+  if (ntiles > 2) issue_tile(IC<2>{}, 2);
+  // The Q fragments must be complete before the loop.  The compiler counts
+  // only its own loads (the DMA is inline asm): left to itself it would place
+  // the Q waits at their first use inside the loop, where each one waits for
+  // every DMA in flight, on every tile.  Using the fragments here puts those
+  // waits before the loop.  They need not cover tile 0 (the compiler may
+  // count spill stores issued after the Q loads): tile 0 is waited for
+  // explicitly.
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) asm volatile("" ::"v"(qf[ks]));
+  if (ntiles > 0) {
+    if (ntiles > 2)
       wait_vmcnt<2 * IPW>();
-    else if (newer == 1)
+    else if (ntiles == 2)
       wait_vmcnt<IPW>();
     else
       wait_vmcnt<0>();
-    barrier_lds();  // tile t landed for every wave; every wave finished tile t-1
-    if (t + 3 < ntiles) issue_tile(t + 3);
-    const int stage = t & (G::STAGES - 1);
-    const int64_t kb = kstart + (int64_t)t * KT;
-    if (wave_active) {
-      bool do_compute = true;
-      if (is_tree) {
-        uint64_t any = 0;
-#pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-          const uint64_t vw = rvalid[rt] ? vis_lds[node_of[rt] * kTreeMaxW + (t >> 1)] : 0ull;
-          any |= (vw >> ((t & 1) * 32)) & 0xffffffffull;
-        }
-        do_compute = __ballot(any != 0ull) != 0ull;
-      }
-      if (do_compute) {
-        // One compute body; masking is a short uniform branch inside it.
-        const bool masked = is_tree || DMASK || (kb + KT > kend);
-        compute(smem + stage * 2 * G::TILE, smem + (stage * 2 + 1) * G::TILE, kb, masked, t);
-      }
-    }
+    barrier_lds();  // tile 0 landed for every wave
+    if (wave_active) s_cur = qk(IC<0>{});
+  }
+  for (int t0 = 0; t0 < ntiles; t0 += 4) {
+    step(IC<0>{}, t0);
+    if (t0 + 1 < ntiles) step(IC<1>{}, t0 + 1);
+    if (t0 + 2 < ntiles) step(IC<2>{}, t0 + 2);
+    if (t0 + 3 < ntiles) step(IC<3>{}, t0 + 3);
   }
 
   // ---- epilogue: normalised bf16 partial + (max, sum) per row ----------------
   if (!wave_active) return;
+  const float ltot = xor32_sum(lsum);
+  if (!rvalid) return;
+  const int64_t prow = (((int64_t)split * a.B + b) * a.Hk + kvh) * a.R + r_me;
+  const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
+  uint16_t* op = a.opart + prow * D;
+  // Accumulator value v of d tile dt holds d = 32*dt + 8*(v/4) + 4*lg + v%4.
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    const float ltot = xor32_sum(lsum[rt]);
-    const int r = row0 + rt * 32 + lj;
-    if (!rvalid[rt]) continue;
-    const int64_t prow = (((int64_t)split * a.B + b) * a.Hk + kvh) * a.R + r;
-    const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
-    uint16_t* op = a.opart + prow * D;
-    // Accumulator value v of d tile dt holds d = 32*dt + 8*(v/4) + 4*lg + v%4.
+  for (int dt = 0; dt < DT; ++dt) {
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const f32x16 x = acc[rt][dt];
-        const u32x2 val = {pack2<BF16>(x[4 * q4] * inv, x[4 * q4 + 1] * inv),
-                           pack2<BF16>(x[4 * q4 + 2] * inv, x[4 * q4 + 3] * inv)};
-        *reinterpret_cast<u32x2*>(op + dt * 32 + 8 * q4 + 4 * lg) = val;
-      }
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const f32x16 x = acc[dt];
+      const u32x2 val = {pack2<BF16>(x[4 * q4] * inv, x[4 * q4 + 1] * inv),
+                         pack2<BF16>(x[4 * q4 + 2] * inv, x[4 * q4 + 3] * inv)};
+      *reinterpret_cast<u32x2*>(op + dt * 32 + 8 * q4 + 4 * lg) = val;
     }
-    if (lg == 0) a.ml[prow] = make_float2(mx[rt], ltot);
   }
+  if (lg == 0) a.ml[prow] = make_float2(mx, ltot);
 }
 
 template <typename T, int D, bool DMASK>
-hipError_t launch_t(const AttnArgs& a, int layout, hipStream_t s) {
+hipError_t launch_t(const AttnArgs& a, hipStream_t s) {
   const int64_t nblk = (int64_t)a.B * a.Hk * a.s_total * a.n_rb;
   if (nblk <= 0) return hipSuccess;
-  const dim3 grid((unsigned)nblk);
-  if (layout == kLayout4x64)
-    hipLaunchKernelGGL((attn_splitk_kernel<T, D, 4, 64, DMASK>), grid, dim3(256), 0, s, a);
-  else if (layout == kLayout8x32)
-    hipLaunchKernelGGL((attn_splitk_kernel<T, D, 8, 32, DMASK>), grid, dim3(512), 0, s, a);
-  else
-    hipLaunchKernelGGL((attn_splitk_kernel<T, D, 4, 32, DMASK>), grid, dim3(256), 0, s, a);
+  hipLaunchKernelGGL((attn_splitk_kernel<T, D, DMASK>), dim3((unsigned)nblk), dim3(512), 0, s, a);
   return hipGetLastError();
 }
 
 template <typename T, bool DMASK>
-hipError_t launch_d(const AttnArgs& a, int D, int layout, hipStream_t s) {
+hipError_t launch_d(const AttnArgs& a, int D, hipStream_t s) {
   switch (D) {
-    case 64: return launch_t<T, 64, DMASK>(a, layout, s);
-    case 128: return launch_t<T, 128, DMASK>(a, layout, s);
+    case 64: return launch_t<T, 64, DMASK>(a, s);
+    case 128: return launch_t<T, 128, DMASK>(a, s);
     default: return hipErrorInvalidValue;
   }
 }
 
 }  // namespace
 
-// Workgroup layouts (waves x rows per wave):
-//   4x32  128 rows, 2 workgroups per CU: the two workgroups on a CU are not
-//         barrier-coupled (measured slower than 8x32 at 64K keys: each
-//         K/V tile feeds half as many rows);
-//   8x32  256 rows, 1 workgroup per CU (2 waves per SIMD, one barrier;
-//         default, fastest measured);
-//   4x64  256 rows, 1 workgroup per CU (1 wave per SIMD, K/V fragments
-//         shared by two row tiles).
-// DSV_ATTN_LAYOUT=432|832|464 overrides the default (for measurements).
-int attn_layout() {
-  static int l = [] {
-    const char* e = getenv("DSV_ATTN_LAYOUT");
-    const int v = e != nullptr ? atoi(e) : 0;
-    return v == 432 ? kLayout4x32 : (v == 464 ? kLayout4x64 : kLayout8x32);
-  }();
-  return l;
-}
-
-int attn_rows_per_block() { return attn_layout() == kLayout4x32 ? 128 : 256; }
-int attn_blocks_per_cu() { return attn_layout() == kLayout4x32 ? 2 : 1; }
+int attn_rows_per_block() { return 256; }
+int attn_blocks_per_cu() { return 1; }
 
 hipError_t launch_attn(const AttnArgs& a, int dtype, int D, bool dmask, hipStream_t s) {
-  const int layout = attn_layout();
-  if (dtype == 0) return dmask ? launch_d<BF16, true>(a, D, layout, s) : launch_d<BF16, false>(a, D, layout, s);
-  return dmask ? launch_d<F16, true>(a, D, layout, s) : launch_d<F16, false>(a, D, layout, s);
+  if (dtype == 0) return dmask ? launch_d<BF16, true>(a, D, s) : launch_d<BF16, false>(a, D, s);
+  return dmask ? launch_d<F16, true>(a, D, s) : launch_d<F16, false>(a, D, s);
 }
 
 }  // namespace dsv

@@ -48,18 +48,45 @@ DSV_HD int64_t src_elem(const KvSrc& s, bool v, int b, int kvh, int64_t n, int64
 }
 
 // How a tile's DMA is issued.
-//   kFast:  scalar base at the instruction's first key (page resolved once),
-//           per-lane offset kii*st + chunk*8, through a bounds-checked buffer
-//           resource; also used for tail tiles with per-lane keys clamped to
-//           the last valid key (an instruction's keys never straddle a page)
-//   kLane:  per-lane full address (keys clamped, page per lane); used when a
-//           page can split an instruction's keys (page < KPI or unaligned key0)
-enum DmaMode : int { kFast = 0, kLane = 1 };
+//   kFast:   scalar base at the instruction's first key (page resolved once),
+//            per-lane offset kii*st + chunk*8, through a bounds-checked buffer
+//            resource; also used for tail tiles with per-lane keys clamped to
+//            the last valid key (an instruction's keys never straddle a page)
+//   kFast32: kFast with the workgroup's batch/head base folded into one
+//            buffer resource per workgroup; per tile only the key's byte
+//            offset from that base changes, in 32-bit arithmetic, added to
+//            the lane offset (the hardware range check covers the sum); the
+//            host selects it when every such offset fits (fast32_ok)
+//   kLane:   per-lane full address (keys clamped, page per lane); used when a
+//            page can split an instruction's keys (page < KPI or unaligned key0)
+enum DmaMode : int { kFast = 0, kLane = 1, kFast32 = 2 };
 
 template <int D>
 DSV_HD int dma_mode(const KvSrc& s) {
-  if (s.pt == nullptr) return kFast;
-  return ((1ll << s.ps_shift) >= Geo<D>::KPI && (s.key0 & (Geo<D>::KPI - 1)) == 0) ? kFast : kLane;
+  const bool fast = s.pt == nullptr || ((1ll << s.ps_shift) >= Geo<D>::KPI && (s.key0 & (Geo<D>::KPI - 1)) == 0);
+  return fast ? (s.fast32 ? kFast32 : kFast) : kLane;
+}
+
+// kFast32: element offset of the workgroup's (batch, head) base, and the byte
+// offset of key n's chunk 0 from that base (page = the key's physical page).
+DSV_HD int64_t wg_base_elem(const KvSrc& s, bool v, int b, int kvh) {
+  return b * (v ? s.v_sb : s.k_sb) + kvh * (v ? s.v_sh : s.k_sh);
+}
+DSV_HD uint32_t tile_off32(const KvSrc& s, bool v, uint32_t n, uint32_t page) {
+  const uint32_t st2 = (uint32_t)(2 * (v ? s.v_st : s.k_st));
+  if (s.pt != nullptr)
+    return page * (uint32_t)(2 * (v ? s.v_sp : s.k_sp)) + (n & ((1u << s.ps_shift) - 1u)) * st2;
+  return n * st2;
+}
+// Host-side choice of kFast32: both views span less than 4 GiB from their
+// base (so every key offset from a workgroup base does too), strides fit,
+// and logical keys up to key_end fit in 31 bits.
+inline bool fast32_ok(const KvSrc& s, int64_t key_end) {
+  const int64_t lim = 1ll << 32;
+  auto fits = [&](int64_t x) { return x >= 0 && 2 * x < lim; };
+  if (s.k_bytes >= lim || s.v_bytes >= lim || key_end >= (1ll << 31)) return false;
+  if (!fits(s.k_st) || !fits(s.v_st)) return false;
+  return s.pt == nullptr || (fits(s.k_sp) && fits(s.v_sp));
 }
 
 // Instruction i of a tile (0..2*NINS-1: K first, then V): which half and block.

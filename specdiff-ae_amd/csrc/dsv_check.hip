@@ -114,7 +114,25 @@ void check_kernel1(const AttnArgs& a, bool dmask, const AttnExtents& ex, Checker
               const int c = is_v ? v_slot(G::CH, key_t, slot) : k_slot(G::CH, key_t, slot);
               ck.cond(c >= 0 && c < G::CH, "chunk index out of range");
               for (int pi = 0; pi < (paged ? 2 : 1); ++pi) {
-                if (mode == kFast) {
+                if (mode == kFast32) {
+                  const int64_t nb = fast_base_key(src, kb, kend, j, G::KPI);
+                  const int64_t nl = fast_lane_key(src, kb, kend, j, G::KPI, kii);
+                  ck.cond(nb >= 0 && nb < (1ll << 31), "key beyond 31 bits in 32-bit mode");
+                  ck.cond(!paged || (nb >> src.ps_shift) == (nl >> src.ps_shift), "DMA instruction straddles a page");
+                  ck.cond(!paged || ((nb >> src.ps_shift) - pt_lo >= 0 && (nb >> src.ps_shift) - pt_lo < kPageLds),
+                          "page slot outside the staged slice");
+                  const int64_t wb = wg_base_elem(src, is_v, b, kvh);
+                  const int64_t le = fast_lane_elem(src, is_v, nb, nl, c);
+                  // The kernel adds a 32-bit lane offset and a 32-bit key offset
+                  // without overflow checks: the true sum must stay below 2^32.
+                  const int64_t off = le * 2 + (int64_t)tile_off32(src, is_v, (uint32_t)nb, (uint32_t)pages[pi]);
+                  ck.cond(le >= 0 && off >= 0 && off + 16 <= 0xffffffffll, "32-bit DMA offset overflow");
+                  ck.cond(off == 2 * (src_elem(src, is_v, b, kvh, nb, pages[pi], 0) - wb) + le * 2,
+                          "32-bit offset differs from the 64-bit address");
+                  const uint32_t range = rsrc_range(is_v ? src.v_bytes : src.k_bytes, wb);
+                  ck.cond(off + 16 <= (int64_t)range, "lane beyond the buffer range");
+                  ck.range(e, elem_addr(base, wb, 2) + (uintptr_t)off, 16, is_v ? "V DMA (fast32)" : "K DMA (fast32)");
+                } else if (mode == kFast) {
                   const int64_t nb = fast_base_key(src, kb, kend, j, G::KPI);
                   const int64_t nl = fast_lane_key(src, kb, kend, j, G::KPI, kii);
                   ck.cond(!paged || (nb >> src.ps_shift) == (nl >> src.ps_shift), "DMA instruction straddles a page");

@@ -45,6 +45,7 @@ struct KvSrc {
   int64_t n_phys;      // physical pages in the pool (page ids are clamped to it)
   int64_t k_bytes;     // byte span of the K (V) tensor view from its base pointer
   int64_t v_bytes;
+  int fast32;          // per-key byte offsets fit in 32 bits (set by the host)
 };
 
 // Arguments of the split-K attention kernel (kernels 1 and 2).
@@ -127,9 +128,7 @@ struct AcceptArgs {
 // Launchers (defined in the .hip files, called by the C-ABI layer).
 // ---------------------------------------------------------------------------
 hipError_t launch_attn(const AttnArgs& a, int dtype, int D, bool dmask, hipStream_t s);
-// Workgroup layout of the attention kernel and what the host plan needs from it.
-enum AttnLayout : int { kLayout4x32 = 0, kLayout8x32 = 1, kLayout4x64 = 2 };
-int attn_layout();
+// What the host plan needs from the attention kernel's workgroup shape.
 int attn_rows_per_block();
 int attn_blocks_per_cu();
 hipError_t launch_merge(const MergeArgs& a, hipStream_t s);
