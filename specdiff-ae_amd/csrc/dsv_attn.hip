@@ -161,6 +161,8 @@ __device__ __forceinline__ bool tmask_keep(const AttnArgs& a, int b, int i, int 
   }
 }
 
+enum KernelMode : int { kModeAny = 0, kModeF32Paged = 1, kModeF32Dense = 2 };
+
 // A compile-time integer: the ring stage of an unrolled loop step, so that
 // every LDS address of the stage folds into an instruction offset.
 template <int N>
@@ -185,7 +187,10 @@ __device__ __forceinline__ float max16(const f32x16& s) {
 // tile t+1's K, and finally O += V(t)^T P(t)^T.  Ring stage of tile t: t & 3;
 // tile t+3 goes into stage (t+3) & 3, whose previous tile (t-1) every wave has
 // finished with once the barrier of iteration t is passed.
-template <typename T, int D, bool DMASK>
+// MODE: kModeF32Paged / kModeF32Dense when both sources are known to use
+// 32-bit DMA offsets (the host checks), else kModeAny (per-source choice at
+// run time).
+template <typename T, int D, bool DMASK, int MODE>
 __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
   using G = Geo<D>;
   constexpr int NW = 8;
@@ -236,8 +241,8 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
   const int64_t nkeys = kend - kstart;
   const int ntiles = nkeys > 0 ? (int)((nkeys + KT - 1) / KT) : 0;
   const int nfull = nkeys > 0 ? (int)(nkeys / KT) : 0;  // tiles without tail keys
-  const bool paged = src.pt != nullptr;
-  const int mode = dma_mode<D>(src);
+  const bool paged = MODE == kModeF32Paged || (MODE == kModeAny && src.pt != nullptr);
+  const int mode = MODE == kModeAny ? dma_mode<D>(src) : (int)kFast32;
 
   // ---- set-up: page-table slice, tree bitmask --------------------------------
   int64_t pt_lo = 0;
@@ -296,14 +301,15 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
     const int c = is_v ? v_slot(CH, key_t, slot) : k_slot(CH, key_t, slot);
     voff_full[x] = (uint32_t)(fast_lane_elem(src, is_v, 0, kii, c) * 2);
   }
-  // kFast32: this workgroup's K and V buffer resources, built once.
-  i32x4 rs_kv[2] = {i32x4{0, 0, 0, 0}, i32x4{0, 0, 0, 0}};
+  // Waves [0, NW/2) issue the K half of each tile's DMA, the others the V
+  // half (NINS is a multiple of IPW, so no wave issues both).
+  const bool dma_v = wid >= NW / 2;
+  // kFast32: the buffer resource of this wave's half for this workgroup,
+  // built once.
+  i32x4 rs = i32x4{0, 0, 0, 0};
   if (mode == kFast32) {
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int64_t wb = wg_base_elem(src, h == 1, b, kvh);
-      rs_kv[h] = make_rsrc((h == 1 ? src.v : src.k) + wb, rsrc_range(h == 1 ? src.v_bytes : src.k_bytes, wb));
-    }
+    const int64_t wb = wg_base_elem(src, dma_v, b, kvh);
+    rs = make_rsrc((dma_v ? src.v : src.k) + wb, rsrc_range(dma_v ? src.v_bytes : src.k_bytes, wb));
   }
   auto issue_tile = [&](auto stage_c, int t) {
     constexpr int stage = decltype(stage_c)::value;
@@ -317,7 +323,7 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
       const int key_t = j * G::KPI + kii;  // key within the tile
       const uint32_t dst = lds_addr(smem + (stage * 2 + (is_v ? 1 : 0)) * G::TILE + j * 1024);
       const uint16_t* base = is_v ? src.v : src.k;
-      if (mode == kFast32) {
+      if (MODE != kModeAny || mode == kFast32) {
         // Keys fit in 31 bits in this mode: per-tile arithmetic is 32-bit scalar.
         const int kb32 = (int)(src.key0 + kb);
         uint32_t nb = (uint32_t)(kb32 + j * G::KPI);
@@ -330,7 +336,9 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
         }
         const uint32_t page =
             paged ? (uint32_t)__builtin_amdgcn_readfirstlane(pt_lds[(int)(nb >> src.ps_shift) - (int)pt_lo]) : 0u;
-        dma_rs(dst, rs_kv[is_v ? 1 : 0], vo + tile_off32(src, is_v, nb, page));
+        KvSrc s32 = src;
+        if (MODE == kModeF32Dense) s32.pt = nullptr;
+        dma_rs(dst, rs, vo + tile_off32(s32, is_v, nb, page));
       } else if (mode == kFast) {
         const int64_t nb = fast_base_key(src, kb, kend, j, G::KPI);
         const int64_t page = paged ? __builtin_amdgcn_readfirstlane(pt_lds[(nb >> src.ps_shift) - pt_lo]) : 0;
@@ -400,17 +408,6 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
     }
   }
 
-  // S^T tile of `stage` (32 keys x this wave's 32 rows).
-  auto qk = [&](auto stage_c) {
-    constexpr int stage = decltype(stage_c)::value;
-    const uint8_t* kt = smem + stage * 2 * G::TILE;
-    f32x16 s = f32x16{};
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      s = mfma32<T>(*reinterpret_cast<const u32x4*>(kt + koff[ks]), qf[ks], s);
-    return s;
-  };
-
   // Keep mask of the scores of tile t (tail keys, tree visibility, byte mask).
   // Bit v of a lane <-> key 4*lg + 8*(v/4) + v%4 of the tile.
   auto mask_scores = [&](f32x16& s, int t) {
@@ -443,24 +440,45 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
     for (int v = 0; v < 16; ++v) s[v] = ((keep >> v) & 1u) ? s[v] : kNegInf;
   };
 
-  // One pipelined step: tile t in ring stage S (t & 3 == S).
-  f32x16 s_cur = f32x16{};
-  auto step = [&](auto stage_c, int t) {
-    constexpr int S = decltype(stage_c)::value;
-    // Tile t+1 landed for every wave; every wave finished tile t-1.
-    if (t + 1 < ntiles) {
-      if (t + 2 < ntiles)
-        wait_vmcnt<IPW>();
-      else
-        wait_vmcnt<0>();
-    }
-    barrier_lds();
-    if (t + 3 < ntiles) issue_tile(IC<(S + 3) & 3>{}, t + 3);
-    if (!wave_active) return;
+  // ---- ping-pong schedule ------------------------------------------------------
+  // Waves [0, NW/2) issue the K half of every tile's DMA, waves [NW/2, NW) the
+  // V half; tile t lives in ring stage t & 3 of the K and V rings.  QK(t) reads
+  // K(t) one interval before PV(t) reads V(t), so K is issued three tiles
+  // ahead and V two: barrier j (one per interval) follows the waits for
+  // K(j+1) and V(j), after it nothing reads K(j-1) or V(j-2) any more, and
+  // K(j+3) / V(j+2) go into those stages.  Two tiles of each stay in flight.
+  //
+  // Every wave runs, per tile k, Y_k (softmax of S(k) -> P(k), VALU) and then
+  // X_k (S(k+1) = QK(k+1) and O += PV(k), MFMA).  K waves meet barrier k
+  // before Y_k, V waves meet barrier k+1 between Y_k and X_k: on each SIMD one
+  // wave is in its MFMA phase while the other is in its VALU phase.
+  const bool v_wave = wid >= NW / 2;
+  static_assert(2 * G::NINS / IPW == NW && G::NINS % IPW == 0, "K and V DMA halves map to wave halves");
 
-    // V^T fragments of tile t.
-    const uint8_t* vt = smem + (S * 2 + 1) * G::TILE;
-    u32x4 vf[2][DT];
+  // The barrier of step k (barrier k for K waves, before Y_k; barrier k+1
+  // for V waves, before X_k), the wait before it and this wave's DMA issue
+  // after it.  K waves: K(k+1) must have landed, K(k+2) may be in flight, and
+  // K(k+3) is issued.  V waves: V(k+1) must have landed, V(k+2) may be in
+  // flight, and V(k+3) is issued.  Either way: tile k+3 into stage (k+3) & 3.
+  auto sync = [&](auto stage3_c, int k) {
+    if (k + 2 < ntiles)
+      wait_vmcnt<IPW>();
+    else
+      wait_vmcnt<0>();
+    barrier_lds();
+    if (k + 3 < ntiles) issue_tile(stage3_c, k + 3);
+  };
+
+  f32x16 s_cur = f32x16{};
+  auto read_k = [&](auto stage_c, u32x4 (&kf)[KS]) {
+    constexpr int stage = decltype(stage_c)::value;
+    const uint8_t* kt = smem + stage * 2 * G::TILE;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) kf[ks] = *reinterpret_cast<const u32x4*>(kt + koff[ks]);
+  };
+  auto read_v = [&](auto stage_c, u32x4 (&vf)[2][DT]) {
+    constexpr int stage = decltype(stage_c)::value;
+    const uint8_t* vt = smem + (stage * 2 + 1) * G::TILE;
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
@@ -471,79 +489,105 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
         const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
         vf[hh][dt] = u32x4{l2[0], l2[1], h2[0], h2[1]};
       }
-
-    if (is_tree || DMASK || t >= nfull) mask_scores(s_cur, t);
-
-    // Online softmax of S(t) (log2 domain, lazy rescale).
-    const float mt = xor32_max(max16(s_cur)) * a.scale_log2;
-    if (__ballot(mt > mx + kRescaleTau) != 0ull) {
-      const float mn = __builtin_elementwise_maximum(mx, mt);
-      const float al = (mn == mx) ? 1.f : __builtin_amdgcn_exp2f(mx - mn);
-      mx = mn;
-      lsum *= al;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) acc[dt] *= al;
-    }
-
-    // S(t+1) on the MFMA pipe (tile t+1 is in stage S+1; past the last tile
-    // the product reads a stale stage and is discarded).
-    const f32x16 s_next = qk(IC<(S + 1) & 3>{});
-
-    const float ms = (mx == kNegInf) ? 0.f : mx;
-    u32x4 pk[2];
-    float ls = lsum;
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      uint32_t w4[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float p0 = __builtin_amdgcn_exp2f(fmaf(s_cur[hh * 8 + 2 * e], a.scale_log2, -ms));
-        const float p1 = __builtin_amdgcn_exp2f(fmaf(s_cur[hh * 8 + 2 * e + 1], a.scale_log2, -ms));
-        w4[e] = pack2<T>(p0, p1);
-        // The normaliser sums the unrounded probabilities: the LSE is an
-        // output in its own right and keeps fp32 accuracy.
-        ls += p0 + p1;
-      }
-      pk[hh] = u32x4{w4[0], w4[1], w4[2], w4[3]};
-    }
-    lsum = ls;
-
-    // O^T += V^T . P^T
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) acc[dt] = mfma32<T>(vf[hh][dt], pk[hh], acc[dt]);
-    s_cur = s_next;
   };
 
-  // ---- main loop: prologue, then steps unrolled over the 4 ring stages --------
+  // Tile k in ring stage S (k & 3 == S).
+  auto step = [&](auto stage_c, int k) {
+    constexpr int S = decltype(stage_c)::value;
+    if (!v_wave && k > 0) sync(IC<(S + 3) & 3>{}, k);
+    u32x4 kf[KS], vf[2][DT];
+    u32x4 pk[2];
+    if (wave_active) {
+      // Operands of X_k, read now so that their latency hides behind Y_k
+      // (past the last tile K(k+1) is a stale stage whose product is unused).
+      read_k(IC<(S + 1) & 3>{}, kf);
+      read_v(IC<S>{}, vf);
+
+      // ---- Y_k: online softmax of S(k) (log2 domain, lazy rescale) ----------
+      if (is_tree || DMASK || k >= nfull) mask_scores(s_cur, k);
+      const float mt = xor32_max(max16(s_cur)) * a.scale_log2;
+      if (__ballot(mt > mx + kRescaleTau) != 0ull) {
+        const float mn = __builtin_elementwise_maximum(mx, mt);
+        const float al = (mn == mx) ? 1.f : __builtin_amdgcn_exp2f(mx - mn);
+        mx = mn;
+        lsum *= al;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) acc[dt] *= al;
+      }
+      const float ms = (mx == kNegInf) ? 0.f : mx;
+      float ls = lsum;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        uint32_t w4[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float p0 = __builtin_amdgcn_exp2f(fmaf(s_cur[hh * 8 + 2 * e], a.scale_log2, -ms));
+          const float p1 = __builtin_amdgcn_exp2f(fmaf(s_cur[hh * 8 + 2 * e + 1], a.scale_log2, -ms));
+          w4[e] = pack2<T>(p0, p1);
+          // The normaliser sums the unrounded probabilities: the LSE is an
+          // output in its own right and keeps fp32 accuracy.
+          ls += p0 + p1;
+        }
+        pk[hh] = u32x4{w4[0], w4[1], w4[2], w4[3]};
+      }
+      lsum = ls;
+    }
+    if (v_wave) sync(IC<(S + 3) & 3>{}, k);
+    if (wave_active) {
+      // ---- X_k: S(k+1) = K(k+1) . Q^T, then O^T += V(k)^T . P(k)^T ----------
+      f32x16 sn = f32x16{};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) sn = mfma32<T>(kf[ks], qf[ks], sn);
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) acc[dt] = mfma32<T>(vf[hh][dt], pk[hh], acc[dt]);
+      s_cur = sn;
+    }
+  };
+
+  // ---- prologue: K(0..2) and V(0..1) issued, barrier 0, S(0) ---------------------
   if (ntiles > 0) issue_tile(IC<0>{}, 0);
   if (ntiles > 1) issue_tile(IC<1>{}, 1);
-  if (ntiles > 2) issue_tile(IC<2>{}, 2);
+  if (ntiles > 2 && !v_wave) issue_tile(IC<2>{}, 2);
   // The Q fragments must be complete before the loop.  The compiler counts
   // only its own loads (the DMA is inline asm): left to itself it would place
   // the Q waits at their first use inside the loop, where each one waits for
   // every DMA in flight, on every tile.  Using the fragments here puts those
-  // waits before the loop.  They need not cover tile 0 (the compiler may
-  // count spill stores issued after the Q loads): tile 0 is waited for
+  // waits before the loop.  They need not cover the DMA (the compiler may
+  // count spill stores issued after the Q loads): the tiles are waited for
   // explicitly.
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) asm volatile("" ::"v"(qf[ks]));
   if (ntiles > 0) {
-    if (ntiles > 2)
-      wait_vmcnt<2 * IPW>();
-    else if (ntiles == 2)
+    // Barrier 0: K(0), K(1) and V(0) landed (K(2) and V(1) may stay in flight).
+    if (v_wave ? ntiles > 1 : ntiles > 2)
       wait_vmcnt<IPW>();
     else
       wait_vmcnt<0>();
-    barrier_lds();  // tile 0 landed for every wave
-    if (wave_active) s_cur = qk(IC<0>{});
+    barrier_lds();
+    if (v_wave) {
+      if (ntiles > 2) issue_tile(IC<2>{}, 2);
+    } else {
+      if (ntiles > 3) issue_tile(IC<3>{}, 3);
+    }
+    if (wave_active) {
+      u32x4 kf[KS];
+      read_k(IC<0>{}, kf);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) s_cur = mfma32<T>(kf[ks], qf[ks], s_cur);
+    }
   }
   for (int t0 = 0; t0 < ntiles; t0 += 4) {
     step(IC<0>{}, t0);
     if (t0 + 1 < ntiles) step(IC<1>{}, t0 + 1);
     if (t0 + 2 < ntiles) step(IC<2>{}, t0 + 2);
     if (t0 + 3 < ntiles) step(IC<3>{}, t0 + 3);
+  }
+  // K waves meet the last barrier (V waves met it after Y of the last tile).
+  if (ntiles > 0 && !v_wave) {
+    wait_vmcnt<0>();
+    barrier_lds();
   }
 
   // ---- epilogue: normalised bf16 partial + (max, sum) per row ----------------
@@ -571,7 +615,20 @@ template <typename T, int D, bool DMASK>
 hipError_t launch_t(const AttnArgs& a, hipStream_t s) {
   const int64_t nblk = (int64_t)a.B * a.Hk * a.s_total * a.n_rb;
   if (nblk <= 0) return hipSuccess;
-  hipLaunchKernelGGL((attn_splitk_kernel<T, D, DMASK>), dim3((unsigned)nblk), dim3(512), 0, s, a);
+  // Both sources in 32-bit mode and of one kind: the specialised kernel.
+  const int mp = dma_mode<D>(a.pre), mt = a.has_tree ? dma_mode<D>(a.tree) : mp;
+  const bool pp = a.pre.pt != nullptr, tp = a.has_tree ? a.tree.pt != nullptr : pp;
+  const dim3 grid((unsigned)nblk), block(512);
+  if constexpr (!DMASK) {
+    if (mp == kFast32 && mt == kFast32 && pp == tp) {
+      if (pp)
+        hipLaunchKernelGGL((attn_splitk_kernel<T, D, DMASK, kModeF32Paged>), grid, block, 0, s, a);
+      else
+        hipLaunchKernelGGL((attn_splitk_kernel<T, D, DMASK, kModeF32Dense>), grid, block, 0, s, a);
+      return hipGetLastError();
+    }
+  }
+  hipLaunchKernelGGL((attn_splitk_kernel<T, D, DMASK, kModeAny>), grid, block, 0, s, a);
   return hipGetLastError();
 }
 
