@@ -123,7 +123,12 @@ __device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t range) {
   r[3] = 0x00020000;
   return r;
 }
-__device__ __forceinline__ void dma_rs(uint32_t lds, i32x4 r, uint32_t voff) {
+__device__ __forceinline__ void dma_rs(uint32_t lds, i32x4 r_in, uint32_t voff) {
+  // Uniform by construction; readfirstlane keeps the resource in SGPRs where
+  // the compiler cannot prove it (free when it already is).
+  i32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = __builtin_amdgcn_readfirstlane(r_in[i]);
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(voff), "s"(r)
                : "memory", "m0");

@@ -6,8 +6,8 @@
 // w_s = l_s * 2^(m_s - M*), the merged row is O = sum_s w_s O_s / sum_s w_s and
 // LSE = ln2 * (M* + log2 sum_s w_s).
 // Lanes are split into (split group, 16-byte column chunk): every lane keeps
-// several independent 16-byte loads in flight, then the split groups are
-// reduced across lanes with DPP-class shuffles.
+// its splits' (m, l) and 16-byte partial loads in flight together, then the
+// split groups are reduced across lanes with DPP-class shuffles.
 // This is the S-way generalisation of the reference's 2-way combine
 // out = O_tree*(1-w) + O_prefix*w with w = sigmoid(lse_prefix - lse_tree)
 // (runtime/tree_attention.py:535-539, llama_target_model.py:862-866), done in
@@ -24,17 +24,6 @@ namespace {
 constexpr float kNegInf = -__builtin_huge_valf();
 constexpr float kLn2 = 0.69314718055994530942f;
 
-__device__ __forceinline__ float wave_max(float x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
-  return x;
-}
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
-  return x;
-}
-
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
@@ -48,10 +37,15 @@ __device__ __forceinline__ void store_val(void* base, int dtype, int64_t off, fl
   }
 }
 
-template <int D>
+// Lanes are (split group sg, 16-byte column chunk tc).  Splits are taken in
+// chunks of SG * SPL: a lane loads the (m, l) pairs and the partial-row chunks
+// of its SPL splits of the chunk at once (one memory round trip per chunk),
+// then the chunk's weights are formed against the running maximum.
+template <int D, int SPL>
 __global__ void __launch_bounds__(256) lse_merge_kernel(const MergeArgs a) {
   constexpr int TPR = D / 8;        // 16-byte column chunks per row
   constexpr int SG = 64 / TPR;      // split groups per wave
+  constexpr int CHUNK = SG * SPL;
   const int lane = threadIdx.x & 63;
   const int tc = lane % TPR, sg = lane / TPR;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -61,41 +55,59 @@ __global__ void __launch_bounds__(256) lse_merge_kernel(const MergeArgs a) {
   const int kvh = (int)((row / a.R) % a.Hk);
   const int b = (int)(row / ((int64_t)a.R * a.Hk));
 
-  // Global max and total weight over splits.
-  float mloc = kNegInf;
-  for (int s = lane; s < a.s_total; s += 64) mloc = fmaxf(mloc, a.ml[s * nrows + row].x);
-  const float mstar = wave_max(mloc);
-  float lloc = 0.f;
-  if (mstar != kNegInf) {
-    for (int s = lane; s < a.s_total; s += 64) {
-      const float2 st = a.ml[s * nrows + row];
-      if (st.x != kNegInf) lloc += __builtin_amdgcn_exp2f(st.x - mstar) * st.y;
-    }
-  }
-  const float L = wave_sum(lloc);
-  const float invL = L > 0.f ? 1.f / L : 0.f;
-
+  float mrun = kNegInf;  // running maximum (log2 units), uniform over the wave
+  float lsum = 0.f;      // this lane's share of sum_s w_s (per split group)
   float acc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-  if (mstar != kNegInf) {
-#pragma unroll 4
-    for (int s = sg; s < a.s_total; s += SG) {
-      const float2 st = a.ml[s * nrows + row];
-      const float w = (st.x == kNegInf) ? 0.f : __builtin_amdgcn_exp2f(st.x - mstar) * st.y;
-      const u32x4 raw = *reinterpret_cast<const u32x4*>(a.opart + (s * nrows + row) * D + tc * 8);
+  for (int s0 = 0; s0 < a.s_total; s0 += CHUNK) {
+    float2 st[SPL];
+    u32x4 raw[SPL];
+#pragma unroll
+    for (int i = 0; i < SPL; ++i) {
+      const int s = s0 + sg + SG * i;
+      if (s < a.s_total) {
+        st[i] = a.ml[s * nrows + row];
+        raw[i] = *reinterpret_cast<const u32x4*>(a.opart + (s * nrows + row) * D + tc * 8);
+      } else {
+        st[i] = make_float2(kNegInf, 0.f);
+        raw[i] = u32x4{0, 0, 0, 0};
+      }
+    }
+    float mc = kNegInf;
+#pragma unroll
+    for (int i = 0; i < SPL; ++i) mc = fmaxf(mc, st[i].x);
+#pragma unroll
+    for (int o = TPR; o < 64; o <<= 1) mc = fmaxf(mc, __shfl_xor(mc, o));
+    const float mnew = fmaxf(mrun, mc);
+    if (mnew == kNegInf) continue;  // nothing visible yet
+    if (mnew != mrun) {
+      const float al = (mrun == kNegInf) ? 0.f : __builtin_amdgcn_exp2f(mrun - mnew);
+      lsum *= al;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] *= al;
+      mrun = mnew;
+    }
+#pragma unroll
+    for (int i = 0; i < SPL; ++i) {
+      const float w = (st[i].x == kNegInf) ? 0.f : __builtin_amdgcn_exp2f(st[i].x - mrun) * st[i].y;
+      lsum += w;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        acc[2 * e] = fmaf(w, bf16_lo(raw[e]), acc[2 * e]);
-        acc[2 * e + 1] = fmaf(w, bf16_hi(raw[e]), acc[2 * e + 1]);
+        acc[2 * e] = fmaf(w, bf16_lo(raw[i][e]), acc[2 * e]);
+        acc[2 * e + 1] = fmaf(w, bf16_hi(raw[i][e]), acc[2 * e + 1]);
       }
     }
   }
+  // Sum over split groups (lanes with the same tc).
 #pragma unroll
   for (int o = TPR; o < 64; o <<= 1) {
+    lsum += __shfl_xor(lsum, o);
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] += __shfl_xor(acc[e], o);
   }
+  const float L = lsum;
+  const float invL = L > 0.f ? 1.f / L : 0.f;
 
   const int g = r / a.M;
   const int mi = r - g * a.M;
@@ -107,7 +119,7 @@ __global__ void __launch_bounds__(256) lse_merge_kernel(const MergeArgs a) {
     for (int e = 0; e < 8; ++e) store_val(a.out, a.out_dtype, obase + e, acc[e] * invL);
   }
   if (lane == 0) {
-    const float lse = (L > 0.f) ? (mstar + __log2f(L)) * kLn2 : kNegInf;
+    const float lse = (L > 0.f) ? (mrun + __log2f(L)) * kLn2 : kNegInf;
     if (a.lse != nullptr) a.lse[(int64_t)b * a.l_sb + (int64_t)m * a.l_sm + (int64_t)h * a.l_sh] = lse;
     if (a.weight != nullptr) {
       const float pl = a.plse[(int64_t)b * a.p_sb + (int64_t)m * a.p_sm + (int64_t)h * a.p_sh];
@@ -124,9 +136,9 @@ hipError_t launch_merge(const MergeArgs& a, hipStream_t s) {
   if (nrows <= 0) return hipSuccess;
   const dim3 grid((unsigned)((nrows + 3) / 4));
   if (a.D == 128)
-    hipLaunchKernelGGL(lse_merge_kernel<128>, grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((lse_merge_kernel<128, 8>), grid, dim3(256), 0, s, a);
   else if (a.D == 64)
-    hipLaunchKernelGGL(lse_merge_kernel<64>, grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((lse_merge_kernel<64, 4>), grid, dim3(256), 0, s, a);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
