@@ -81,6 +81,21 @@ class HipEvents:
             self.hip.hipEventDestroy(e)
 
 
+def measured_traffic():
+    """HBM bytes per kernel-1 launch from the committed rocprofv3 counter passes.
+
+    profiles/attn_splitk_64k_traffic.json holds FETCH_SIZE and WRITE_SIZE (KiB
+    per dispatch) of kernel 1 on this workload and of a 1 GiB device copy, with
+    the commands that produced them; each counter is scaled by bytes / counter
+    of the copy.  Returns None when the file is absent.
+    """
+    f = REPO / "profiles" / "attn_splitk_64k_traffic.json"
+    if not f.exists():
+        return None
+    d = json.loads(f.read_text())
+    return int(d["kernel_fetch_kib"] * 1024 * d["fetch_scale"] + d["kernel_write_kib"] * 1024 * d["write_scale"])
+
+
 def bench_verify(args, lib, ev):
     from diffspec_mi355x import workloads as wl
     from diffspec_mi355x.runtime.tree_attention import tree_verify
@@ -186,6 +201,9 @@ def main():
     ap.add_argument("--cpu-max-steps", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-accept", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 1 GiB device-to-device copy (scale reference for the FETCH_SIZE / WRITE_SIZE "
+                         "counters) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (got --gpus {args.gpus}). "
@@ -194,6 +212,16 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(1)
+
+    if args.copy_calibration:
+        n = 1 << 30
+        src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_read": n, "copy_calibration_bytes_written": n}), flush=True)
+        return
 
     from diffspec_mi355x import _ext
 
@@ -227,7 +255,7 @@ def main():
         "hbm_frac_step": round(nb["step"] / (us_step * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
         "roofline": {"kernel": "attn_splitk_kernel (kernel 1: prefix splits + tree split)", "bound": "hbm",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "bytes_per_launch": nb["kernel1"], "avg_us": round(k1_us, 3), "median_us": round(k1_med, 3)},
         "wall_s_timed": round(t_wall, 4),
     }
