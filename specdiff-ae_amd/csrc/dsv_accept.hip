@@ -180,6 +180,208 @@ __global__ void __launch_bounds__(kRowThreads) accept_rowstat_kernel(const Accep
   }
 }
 
+// ---------------------------------------------------------------------------
+// Stage A for 16-bit logits (bf16 / f16), rows 16-byte aligned.
+//
+// A 16-bit float maps to an unsigned key that orders like the value:
+// key = bits ^ (bits < 0 ? 0xFFFF : 0x8000) (sign-magnitude -> offset), so
+// the argmax is "largest key, then lowest index".  Keys are formed two per
+// dword with packed 16-bit ops (v_pk_ashrrev_i16 / v_pk_max_u16), the chunk's
+// maximum key is reduced over the workgroup, and a second pass over the
+// register-resident data finds the first index holding it (a thread that has
+// a hit - rare - locates it with a scalar scan).  A chunk containing a NaN
+// takes an exact slow path in which every NaN gets the largest key (torch
+// ranks NaN above all numbers, first index wins).  Typical statistics reuse
+// the chunk maximum as m, so one exp2, two FMAs and an add per element remain.
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+typedef short i16x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kVecPerThread = 8;  // 16-byte vectors per thread (chunk <= 256 * 8 * 8 elements)
+
+__device__ __forceinline__ uint32_t key2(uint32_t x) {
+  const i16x2 sx = __builtin_bit_cast(i16x2, x);
+  const i16x2 sgn = sx >> (short)15;  // 0xFFFF for negative halves
+  return x ^ (__builtin_bit_cast(uint32_t, sgn) | 0x80008000u);
+}
+__device__ __forceinline__ uint32_t pk_max(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, a), __builtin_bit_cast(u16x2, b)));
+}
+__device__ __forceinline__ uint32_t pk_min(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_min(__builtin_bit_cast(u16x2, a), __builtin_bit_cast(u16x2, b)));
+}
+template <bool F16>
+__device__ __forceinline__ float half_to_f(uint32_t h) {
+  if constexpr (F16) return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+  return __uint_as_float(h << 16);
+}
+__device__ __forceinline__ uint32_t key_to_bits(uint32_t k) { return (k & 0x8000u) ? (k ^ 0x8000u) : (~k & 0xFFFFu); }
+
+template <bool F16, bool TYPICAL>
+__global__ void __launch_bounds__(kRowThreads) accept_rowstat16_kernel(const AcceptArgs a) {
+  constexpr uint32_t kNanAbove = F16 ? 0x7C00u : 0x7F80u;  // |bits| above: NaN
+  constexpr uint32_t kNegInfBits = F16 ? 0xFC00u : 0xFF80u;
+  constexpr int kNw = kRowThreads / 64;
+  const int c = blockIdx.x;
+  const int64_t row = blockIdx.y;  // t * M + i
+  const int t = (int)(row / a.M), i = (int)(row % a.M);
+  const uint16_t* base = reinterpret_cast<const uint16_t*>(a.logits) + (int64_t)t * a.l_st + (int64_t)i * a.l_sm;
+  const int64_t lo = (int64_t)c * a.chunk;
+  const int n = (int)(min(lo + a.chunk, a.V) - lo);
+  const int nvec = n >> 3;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  __shared__ uint32_t red_u[kNw];
+  __shared__ float red_l[kNw], red_s[kNw];
+
+  // Vector v of this thread covers chunk elements [8 * (tid + 256 v), +8);
+  // vectors past the chunk hold -inf (they come after every real element).
+  const uint32_t pad = kNegInfBits | (kNegInfBits << 16);
+  u32x4 raw[kVecPerThread];
+#pragma unroll
+  for (int v = 0; v < kVecPerThread; ++v) {
+    const int vi = tid + kRowThreads * v;
+    raw[v] = vi < nvec ? *reinterpret_cast<const u32x4*>(base + lo + 8 * vi) : u32x4{pad, pad, pad, pad};
+  }
+  // Elements past the last whole vector (n % 8 of them), one per thread.
+  const int ntail = n - 8 * nvec;
+  uint32_t tail_bits = kNegInfBits;
+  if (tid < ntail) tail_bits = base[lo + 8 * nvec + tid];
+
+  // NaN anywhere in the chunk?
+  uint32_t amax = tail_bits & 0x7FFFu;
+#pragma unroll
+  for (int v = 0; v < kVecPerThread; ++v)
+#pragma unroll
+    for (int w = 0; w < 4; ++w) amax = pk_max(amax, raw[v][w] & 0x7FFF7FFFu);
+  amax = max(amax & 0xFFFFu, amax >> 16);
+  const bool chunk_nan = __syncthreads_or(amax > kNanAbove) != 0;
+
+  // Largest key.
+  uint32_t kbest = 0;
+  if (!chunk_nan) {
+#pragma unroll
+    for (int v = 0; v < kVecPerThread; ++v)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) kbest = pk_max(kbest, key2(raw[v][w]));
+    kbest = max(kbest & 0xFFFFu, kbest >> 16);
+    kbest = max(kbest, key2(tail_bits) & 0xFFFFu);
+  } else {
+    // Exact path: NaN halves take the largest key.
+    auto nkey = [&](uint32_t h) { return (h & 0x7FFFu) > kNanAbove ? 0xFFFFu : (key2(h) & 0xFFFFu); };
+#pragma unroll
+    for (int v = 0; v < kVecPerThread; ++v)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) kbest = max(kbest, max(nkey(raw[v][w] & 0xFFFFu), nkey(raw[v][w] >> 16)));
+    kbest = max(kbest, nkey(tail_bits));
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) kbest = max(kbest, (uint32_t)__shfl_xor((int)kbest, o));
+  if (lane == 0) red_u[wv] = kbest;
+  __syncthreads();
+  uint32_t kstar = red_u[0];
+#pragma unroll
+  for (int x = 1; x < kNw; ++x) kstar = max(kstar, red_u[x]);
+  __syncthreads();
+
+  // A zero maximum: -0 and +0 compare equal (keys 0x7FFF and 0x8000), so
+  // both count as hits and the exact scan runs.
+  const bool zmax = !chunk_nan && (kstar == 0x7FFFu || kstar == 0x8000u);
+  if (zmax) kstar = 0x8000u;
+
+  // First index holding kstar.
+  int first = 0x7fffffff;
+  {
+    auto hkey = [&](uint32_t h) {
+      const uint32_t k = chunk_nan && (h & 0x7FFFu) > kNanAbove ? 0xFFFFu : (key2(h) & 0xFFFFu);
+      return (zmax && k == 0x7FFFu) ? 0x8000u : k;
+    };
+    bool hit;
+    if (!chunk_nan && !zmax) {
+      const uint32_t kk = kstar | (kstar << 16);
+      uint32_t accz = 0x00010001u;
+#pragma unroll
+      for (int v = 0; v < kVecPerThread; ++v)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) accz &= pk_min(key2(raw[v][w]) ^ kk, 0x00010001u);
+      hit = accz != 0x00010001u;
+    } else {
+      hit = true;
+    }
+    if (hit) {
+      for (int v = 0; v < kVecPerThread && first == 0x7fffffff; ++v) {
+        const int vi = tid + kRowThreads * v;
+        if (vi >= nvec) break;
+        for (int w = 0; w < 8; ++w) {
+          const uint32_t h = (raw[v][w >> 1] >> (16 * (w & 1))) & 0xFFFFu;
+          if (hkey(h) == kstar) {
+            first = 8 * vi + w;
+            break;
+          }
+        }
+      }
+    }
+    if (first == 0x7fffffff && tid < ntail && hkey(tail_bits) == kstar) first = 8 * nvec + tid;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) first = min(first, __shfl_xor(first, o));
+  if (lane == 0) red_u[wv] = (uint32_t)first;
+  __syncthreads();
+  int fbest = (int)red_u[0];
+#pragma unroll
+  for (int x = 1; x < kNw; ++x) fbest = min(fbest, (int)red_u[x]);
+
+  const float vbest = chunk_nan && kstar == 0xFFFFu ? __builtin_nanf("") : half_to_f<F16>(key_to_bits(kstar));
+
+  // Typical statistics against m = max(x) * log2(e) / T.
+  float mz = kNegInf, lsum = 0.f, ssum = 0.f;
+  if constexpr (TYPICAL) {
+    const float zs = a.inv_temp * kLog2e;
+    mz = vbest * zs;
+    if (mz != kNegInf) {
+      float l = 0.f, sx = 0.f;
+#pragma unroll
+      for (int v = 0; v < kVecPerThread; ++v)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const float x0 = half_to_f<F16>(raw[v][w] & 0xFFFFu), x1 = half_to_f<F16>(raw[v][w] >> 16);
+          const float p0 = __builtin_amdgcn_exp2f(fmaf(x0, zs, -mz));
+          const float p1 = __builtin_amdgcn_exp2f(fmaf(x1, zs, -mz));
+          l += p0 + p1;
+          sx = fmaf(x0, p0, fmaf(x1, p1, sx));
+        }
+      if (tid < ntail) {
+        const float x = half_to_f<F16>(tail_bits);
+        const float p = __builtin_amdgcn_exp2f(fmaf(x, zs, -mz));
+        l += p;
+        sx = fmaf(x, p, sx);
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        l += __shfl_xor(l, o);
+        sx += __shfl_xor(sx, o);
+      }
+      __syncthreads();
+      if (lane == 0) {
+        red_l[wv] = l;
+        red_s[wv] = sx;
+      }
+      __syncthreads();
+      lsum = red_l[0];
+      ssum = red_s[0];
+#pragma unroll
+      for (int x = 1; x < kNw; ++x) {
+        lsum += red_l[x];
+        ssum += red_s[x];
+      }
+      ssum *= a.inv_temp;
+    }
+  }
+  if (tid == 0) {
+    const int64_t o = row * a.nchunk + c;
+    a.rstat[o] = make_float4(vbest, __int_as_float((int)(lo + fbest)), mz, lsum);
+    if constexpr (TYPICAL) a.rstat2[o] = ssum;
+  }
+}
+
 __global__ void __launch_bounds__(1024) accept_walk_kernel(const AcceptArgs a) {
   extern __shared__ int64_t smem64[];
   const int M = a.M;
@@ -345,6 +547,16 @@ __global__ void __launch_bounds__(1024) accept_walk_kernel(const AcceptArgs a) {
   }
 }
 
+template <bool F16>
+hipError_t launch_rowstat16(const AcceptArgs& a, hipStream_t s) {
+  dim3 grid((unsigned)a.nchunk, (unsigned)((int64_t)a.T * a.M));
+  if (a.mode == 1)
+    hipLaunchKernelGGL((accept_rowstat16_kernel<F16, true>), grid, dim3(kRowThreads), 0, s, a);
+  else
+    hipLaunchKernelGGL((accept_rowstat16_kernel<F16, false>), grid, dim3(kRowThreads), 0, s, a);
+  return hipGetLastError();
+}
+
 template <typename LT>
 hipError_t launch_rowstat(const AcceptArgs& a, hipStream_t s) {
   dim3 grid((unsigned)a.nchunk, (unsigned)((int64_t)a.T * a.M));
@@ -366,10 +578,14 @@ hipError_t launch_accept(const AcceptArgs& a, hipStream_t s, hipEvent_t ev0, hip
   if (a.T <= 0 || a.M <= 0) return hipSuccess;
   hipError_t e;
   if (ev0 != nullptr && (e = hipEventRecord(ev0, s)) != hipSuccess) return e;
+  // 16-bit logits with 16-byte aligned rows and chunks take the packed-key
+  // kernel (its chunk must fit 256 threads x 8 vectors of 8 elements).
+  const bool al16 = ((uintptr_t)a.logits & 15) == 0 && (a.l_st * 2) % 16 == 0 && (a.l_sm * 2) % 16 == 0 &&
+                    (a.chunk * 2) % 16 == 0 && a.chunk <= (int64_t)kRowThreads * kVecPerThread * 8;
   if (a.l_dtype == 0)
-    e = launch_rowstat<uint16_t>(a, s);
+    e = al16 ? launch_rowstat16<false>(a, s) : launch_rowstat<uint16_t>(a, s);
   else if (a.l_dtype == 1)
-    e = launch_rowstat<_Float16>(a, s);
+    e = al16 ? launch_rowstat16<true>(a, s) : launch_rowstat<_Float16>(a, s);
   else
     e = launch_rowstat<float>(a, s);
   if (e != hipSuccess) return e;

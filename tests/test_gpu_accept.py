@@ -157,3 +157,46 @@ def test_verify_new_contract_with_kv_compaction(gpu):
     for x, x0 in zip(kv, kv_before):
         assert torch.equal(x[..., start:start + len(w[1]), :], x0[..., sel, :])
     assert model.draft_model.last_bundle_stats["num_bundles"] >= 1
+
+
+def _edge_rows(V):
+    """Rows that exercise the ordering of 16-bit keys (V a multiple of 8, so
+    rows are 16-byte aligned and the packed-key sweep runs)."""
+    g = torch.Generator().manual_seed(11)
+    lg = torch.randn((7, V), generator=g)
+    lg[0] = -lg[0].abs() - 1.0                     # all negative
+    lg[1, 2] = lg[1, 3] = lg[1, 1000] = 9.0        # ties inside one dword and across threads
+    lg[2] = -1.0
+    lg[2, 5] = -0.0                                # -0 == +0: first one wins
+    lg[2, 9] = 0.0
+    lg[3] = float("-inf")                          # all -inf: index 0
+    lg[4, 100] = lg[4, V - 3] = float("inf")       # +inf ties across chunks
+    lg[5, 20] = lg[5, V - 10] = float("nan")       # first NaN wins
+    return lg
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_packed_key_sweep_edge_rows(gpu, dtype):
+    V = 16384 * 2 + 8 * 41
+    lg = _edge_rows(V).to(dtype)
+    M = lg.shape[0]
+    want = torch.argmax(lg.float(), -1).tolist()
+    r = tree_accept(lg.unsqueeze(0).to(gpu), torch.zeros((1, M), dtype=torch.int64, device=gpu),
+                    torch.full((1, M - 1), -1, dtype=torch.int64, device=gpu), torch.arange(M, device=gpu), 4,
+                    return_next=True)
+    assert r["next"][0].cpu().tolist() == want
+
+
+def test_packed_key_sweep_strided_rows_with_short_tail(gpu):
+    # rows of a wider, 16-byte aligned buffer: the vocab tail (V % 8 != 0) is
+    # read by the scalar tail path of the packed-key sweep
+    a = wl.make_accept_inputs(T=2, M=24, V=16384 + 8 * 300 + 5, dtype=torch.bfloat16, device=str(gpu), seed=9)
+    V = a.logits.shape[-1]
+    wide = torch.full((2, 24, V + 3), -100.0, dtype=torch.bfloat16, device=gpu)
+    wide[..., :V] = a.logits
+    wide[1, 5, V - 2] = 50.0                       # maximum inside the tail
+    lg = wide[..., :V]
+    assert lg.stride(1) * 2 % 16 == 0
+    run_and_compare(lg, a.draft, a.parent_ref, a.pos, 8)
+    run_and_compare(lg, a.draft, a.parent_ref, a.pos, 8, mode="typical", temperature=1.0,
+                    posterior_threshold=0.09, posterior_alpha=0.3)
