@@ -250,10 +250,10 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
   const int mode = MODE == kModeAny ? dma_mode<D>(src) : (int)kFast32;
 
   // ---- set-up: page-table slice, tree bitmask --------------------------------
-  int64_t pt_lo = 0;
+  int64_t pt_lo = 0, pt_hi = -1;
   if (paged && ntiles > 0) {
     pt_lo = (src.key0 + kstart) >> src.ps_shift;
-    const int64_t pt_hi = (src.key0 + kend - 1) >> src.ps_shift;
+    pt_hi = (src.key0 + kend - 1) >> src.ps_shift;
     for (int64_t i = tid; i <= pt_hi - pt_lo; i += NT)
       pt_lds[i] = (int32_t)clamp_page(load_index(src.pt, src.pt_i64, b * src.pt_sb + pt_lo + i), src.n_phys);
   }
@@ -316,8 +316,55 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
     const int64_t wb = wg_base_elem(src, dma_v, b, kvh);
     rs = make_rsrc((dma_v ? src.v : src.k) + wb, rsrc_range(dma_v ? src.v_bytes : src.k_bytes, wb));
   }
+  // Page window (32-bit paged mode): lane l of pgw[x] holds the physical page
+  // of this wave's DMA instruction x in full tile pgw_t0 + l, so that a tile's
+  // page costs a lane read instead of an LDS round trip; the window is
+  // refilled from the LDS page-table slice once per 64 tiles.
+  uint32_t pgw[IPW];
+  int pgw_t0 = -64;
+#pragma unroll
+  for (int x = 0; x < IPW; ++x) pgw[x] = 0;
+  auto fill_pgw = [&](int t0) {
+    pgw_t0 = t0;
+    const int last = (int)(pt_hi - pt_lo);
+#pragma unroll
+    for (int x = 0; x < IPW; ++x) {
+      bool is_v;
+      int j;
+      dma_ins<D>(wid * IPW + x, is_v, j);
+      const uint32_t nb = (uint32_t)(src.key0 + kstart) + (uint32_t)(t0 + lane) * KT + (uint32_t)(j * G::KPI);
+      const int e = min((int)(nb >> src.ps_shift) - (int)pt_lo, last);  // lanes past the split: any valid entry
+      pgw[x] = (uint32_t)pt_lds[e];
+    }
+  };
+
+  // 32-bit modes: this wave's half (K or V) byte strides, uniform.
+  const uint32_t key0_32 = (uint32_t)(src.key0 + kstart);
+  const uint32_t st2 = (uint32_t)__builtin_amdgcn_readfirstlane((int)(2 * (dma_v ? src.v_st : src.k_st)));
+  const uint32_t sp2 = (uint32_t)__builtin_amdgcn_readfirstlane((int)(2 * (dma_v ? src.v_sp : src.k_sp)));
+  const uint32_t psm = (1u << src.ps_shift) - 1u;
+  KvSrc s32 = src;
+  if (MODE == kModeF32Dense) s32.pt = nullptr;
+
   auto issue_tile = [&](auto stage_c, int t) {
     constexpr int stage = decltype(stage_c)::value;
+    if (MODE != kModeAny && t < nfull) {
+      // Full tile in a 32-bit mode: scalar key arithmetic, the lane offsets of
+      // voff_full, the page from the window.
+      if (MODE == kModeF32Paged && t - pgw_t0 >= 64) fill_pgw(t);
+      const uint32_t nbt = key0_32 + (uint32_t)t * KT;
+#pragma unroll
+      for (int x = 0; x < IPW; ++x) {
+        bool is_v;
+        int j;
+        dma_ins<D>(wid * IPW + x, is_v, j);
+        const uint32_t dst = lds_addr(smem + (stage * 2 + (is_v ? 1 : 0)) * G::TILE + j * 1024);
+        const uint32_t page =
+            MODE == kModeF32Paged ? (uint32_t)__builtin_amdgcn_readlane((int)pgw[x], t - pgw_t0) : 0u;
+        dma_rs(dst, rs, voff_full[x] + tile_off32_s(MODE == kModeF32Paged, st2, sp2, psm, nbt + (uint32_t)(j * G::KPI), page));
+      }
+      return;
+    }
     const int64_t kb = kstart + (int64_t)t * KT;
     const bool full = t < nfull;
 #pragma unroll
@@ -341,8 +388,6 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
         }
         const uint32_t page =
             paged ? (uint32_t)__builtin_amdgcn_readfirstlane(pt_lds[(int)(nb >> src.ps_shift) - (int)pt_lo]) : 0u;
-        KvSrc s32 = src;
-        if (MODE == kModeF32Dense) s32.pt = nullptr;
         dma_rs(dst, rs, vo + tile_off32(s32, is_v, nb, page));
       } else if (mode == kFast) {
         const int64_t nb = fast_base_key(src, kb, kend, j, G::KPI);
@@ -384,6 +429,9 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) qf[ks] = u32x4{0, 0, 0, 0};
   }
+
+  // Score scale (log2 units), a kernel argument held in an SGPR for the loop.
+  const float scale_log2 = a.scale_log2;
 
   f32x16 acc[DT];
   float mx = kNegInf, lsum = 0.f;
@@ -510,7 +558,7 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
 
       // ---- Y_k: online softmax of S(k) (log2 domain, lazy rescale) ----------
       if (is_tree || DMASK || k >= nfull) mask_scores(s_cur, k);
-      const float mt = xor32_max(max16(s_cur)) * a.scale_log2;
+      const float mt = xor32_max(max16(s_cur)) * scale_log2;
       if (__ballot(mt > mx + kRescaleTau) != 0ull) {
         const float mn = __builtin_elementwise_maximum(mx, mt);
         const float al = (mn == mx) ? 1.f : __builtin_amdgcn_exp2f(mx - mn);
@@ -526,8 +574,8 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
         uint32_t w4[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float p0 = __builtin_amdgcn_exp2f(fmaf(s_cur[hh * 8 + 2 * e], a.scale_log2, -ms));
-          const float p1 = __builtin_amdgcn_exp2f(fmaf(s_cur[hh * 8 + 2 * e + 1], a.scale_log2, -ms));
+          const float p0 = __builtin_amdgcn_exp2f(fmaf(s_cur[hh * 8 + 2 * e], scale_log2, -ms));
+          const float p1 = __builtin_amdgcn_exp2f(fmaf(s_cur[hh * 8 + 2 * e + 1], scale_log2, -ms));
           w4[e] = pack2<T>(p0, p1);
           // The normaliser sums the unrounded probabilities: the LSE is an
           // output in its own right and keeps fp32 accuracy.
@@ -564,6 +612,11 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
   // explicitly.
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) asm volatile("" ::"v"(qf[ks]));
+  // The same holds for the scalar load of the score scale: the counter that
+  // tracks it also tracks the LDS operand reads, so a first wait inside the
+  // loop would wait for every operand read of the tile, ahead of the softmax
+  // that is meant to hide their latency.
+  asm volatile("" ::"s"(scale_log2));
   if (ntiles > 0) {
     // Barrier 0: K(0), K(1) and V(0) landed (K(2) and V(1) may stay in flight).
     if (v_wave ? ntiles > 1 : ntiles > 2)

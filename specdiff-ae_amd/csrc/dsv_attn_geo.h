@@ -72,11 +72,14 @@ DSV_HD int dma_mode(const KvSrc& s) {
 DSV_HD int64_t wg_base_elem(const KvSrc& s, bool v, int b, int kvh) {
   return b * (v ? s.v_sb : s.k_sb) + kvh * (v ? s.v_sh : s.k_sh);
 }
+// The same with the half's byte strides given (st2 = 2*st, sp2 = 2*sp,
+// psm = page_size - 1) and the paging known.
+DSV_HD uint32_t tile_off32_s(bool paged, uint32_t st2, uint32_t sp2, uint32_t psm, uint32_t n, uint32_t page) {
+  return paged ? page * sp2 + (n & psm) * st2 : n * st2;
+}
 DSV_HD uint32_t tile_off32(const KvSrc& s, bool v, uint32_t n, uint32_t page) {
-  const uint32_t st2 = (uint32_t)(2 * (v ? s.v_st : s.k_st));
-  if (s.pt != nullptr)
-    return page * (uint32_t)(2 * (v ? s.v_sp : s.k_sp)) + (n & ((1u << s.ps_shift) - 1u)) * st2;
-  return n * st2;
+  return tile_off32_s(s.pt != nullptr, (uint32_t)(2 * (v ? s.v_st : s.k_st)), (uint32_t)(2 * (v ? s.v_sp : s.k_sp)),
+                      (1u << s.ps_shift) - 1u, n, page);
 }
 // Host-side choice of kFast32: both views span less than 4 GiB from their
 // base (so every key offset from a workgroup base does too), strides fit,
