@@ -100,7 +100,8 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
-// LDS-DMA: 16 bytes per lane, lane l lands at LDS m0 + 16*l.
+// LDS-DMA: 16 bytes per lane, lane l lands at LDS m0 + 16*l.  K/V bytes are
+// read once per verify step: the loads are marked non-temporal (nt).
 // Through a buffer resource (hardware range check; out-of-range lanes read 0).
 __device__ __forceinline__ void dma_buf(uint32_t lds, const void* base, uint32_t range, uint32_t voff) {
   const uint64_t p = (uint64_t)base;
@@ -110,7 +111,7 @@ __device__ __forceinline__ void dma_buf(uint32_t lds, const void* base, uint32_t
   r[2] = __builtin_amdgcn_readfirstlane((int)range);
   r[3] = 0x00020000;
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(voff), "s"(r)
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds" ::"s"(m0), "v"(voff), "s"(r)
                : "memory", "m0");
 }
 // A buffer resource (base, byte range) in SGPRs, built once and reused.
@@ -130,13 +131,13 @@ __device__ __forceinline__ void dma_rs(uint32_t lds, i32x4 r_in, uint32_t voff) 
 #pragma unroll
   for (int i = 0; i < 4; ++i) r[i] = __builtin_amdgcn_readfirstlane(r_in[i]);
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0), "v"(voff), "s"(r)
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds" ::"s"(m0), "v"(voff), "s"(r)
                : "memory", "m0");
 }
 // With a full per-lane address (keys clamped to valid ones by the caller).
 __device__ __forceinline__ void dma_lane(uint32_t lds, const void* vaddr) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(vaddr) : "memory", "m0");
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off nt" ::"s"(m0), "v"(vaddr) : "memory", "m0");
 }
 
 // Wait until at most N of this wave's vector-memory operations are pending.
