@@ -70,7 +70,8 @@ def softmax_stats(row: np.ndarray, temperature: float = 1.0) -> Tuple[np.ndarray
     e = np.exp(y - m)
     z = e.sum()
     p = e / z
-    ent = float(m + np.log(z) - (p * y).sum())
+    # 0 log 0 = 0: entries with p = 0 (y = -inf) add nothing to sum p*y.
+    ent = float(m + np.log(z) - (p * np.where(p > 0, y, 0.0)).sum())
     return p, ent
 
 

@@ -23,6 +23,8 @@
 // with the posterior criterion of Cai et al. 2024 (Medusa, typical acceptance):
 //   p_T(draft[i] | parent) > min(eps, alpha * exp(-H(p_T(. | parent)))).
 
+#include <algorithm>
+
 #include "dsv_internal.h"
 
 namespace dsv {
@@ -109,7 +111,8 @@ __global__ void __launch_bounds__(kRowThreads) accept_rowstat_kernel(const Accep
         for (int e = 0; e < n; ++e) {
           const float p = __builtin_amdgcn_exp2f(fmaf(xs[e], zs, -sm.m));
           sm.l += p;
-          sm.s = fmaf(xs[e] * a.inv_temp, p, sm.s);
+          // 0 log 0 = 0: a -inf logit (p = 0) adds nothing to s.
+          if (p > 0.f) sm.s = fmaf(xs[e] * a.inv_temp, p, sm.s);
         }
       }
     }
@@ -181,22 +184,36 @@ __global__ void __launch_bounds__(kRowThreads) accept_rowstat_kernel(const Accep
 }
 
 // ---------------------------------------------------------------------------
-// Stage A for 16-bit logits (bf16 / f16), rows 16-byte aligned.
+// Stage A for 16-bit logits (bf16 / f16), rows 16-byte aligned: streaming.
 //
 // A 16-bit float maps to an unsigned key that orders like the value:
 // key = bits ^ (bits < 0 ? 0xFFFF : 0x8000) (sign-magnitude -> offset), so
 // the argmax is "largest key, then lowest index".  Keys are formed two per
-// dword with packed 16-bit ops (v_pk_ashrrev_i16 / v_pk_max_u16), the chunk's
-// maximum key is reduced over the workgroup, and a second pass over the
-// register-resident data finds the first index holding it (a thread that has
-// a hit - rare - locates it with a scalar scan).  A chunk containing a NaN
-// takes an exact slow path in which every NaN gets the largest key (torch
-// ranks NaN above all numbers, first index wins).  Typical statistics reuse
-// the chunk maximum as m, so one exp2, two FMAs and an add per element remain.
+// dword with packed 16-bit ops (v_pk_ashrrev_i16 / v_pk_max_u16).
+//
+// A workgroup covers a contiguous vocabulary range of one row and streams it
+// in sub-tiles of kSub elements, the loads of sub-tile s+1 in flight while
+// sub-tile s is reduced.  A thread's elements have increasing indices from
+// sub-tile to sub-tile, so each thread keeps running statistics:
+//   * the largest key and the first index holding it: only a strictly larger
+//     key of a later sub-tile replaces it, and the index is then located by
+//     a scan of the thread's 32 elements (rare after the first sub-tiles);
+//   * the first NaN index (torch ranks NaN above every number; a range with
+//     a NaN reports NaN at its first NaN, and NaN typical statistics);
+//   * typical: (m, l, s) against the thread's running maximum, rescaled when
+//     it grows (online softmax).  -inf logits contribute p = 0 and, by
+//     0 log 0 = 0, nothing to s: they are clamped to the lowest finite value
+//     (their exponential underflows to exactly 0) before the products.
+// The workgroup then reduces the thread statistics.  -0 and +0 compare equal
+// (keys 0x7FFF and 0x8000): a range whose maximum is +0 is rescanned from
+// memory for the first zero of either sign (exact, and rare).
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 typedef short i16x2 __attribute__((ext_vector_type(2)));
 
-constexpr int kVecPerThread = 8;  // 16-byte vectors per thread (chunk <= 256 * 8 * 8 elements)
+constexpr int kStrThreads = 256;
+constexpr int kStrVec = 4;                                   // 16-byte vectors per thread per sub-tile
+constexpr int kSubVec = kStrThreads * kStrVec;               // vectors per sub-tile
+constexpr int64_t kSub = (int64_t)kSubVec * 8;               // elements per sub-tile
 
 __device__ __forceinline__ uint32_t key2(uint32_t x) {
   const i16x2 sx = __builtin_bit_cast(i16x2, x);
@@ -217,167 +234,260 @@ __device__ __forceinline__ float half_to_f(uint32_t h) {
 __device__ __forceinline__ uint32_t key_to_bits(uint32_t k) { return (k & 0x8000u) ? (k ^ 0x8000u) : (~k & 0xFFFFu); }
 
 template <bool F16, bool TYPICAL>
-__global__ void __launch_bounds__(kRowThreads) accept_rowstat16_kernel(const AcceptArgs a) {
-  constexpr uint32_t kNanAbove = F16 ? 0x7C00u : 0x7F80u;  // |bits| above: NaN
+__global__ void __launch_bounds__(kStrThreads) accept_stream16_kernel(const AcceptArgs a) {
+  constexpr uint32_t kNanAbove = F16 ? 0x7C00u : 0x7F80u;    // |bits| above: NaN
   constexpr uint32_t kNegInfBits = F16 ? 0xFC00u : 0xFF80u;
-  constexpr int kNw = kRowThreads / 64;
+  constexpr uint32_t kLowest2 = F16 ? 0xFBFFFBFFu : 0xFF7FFF7Fu;  // lowest finite, both halves
+  constexpr int kNw = kStrThreads / 64;
   const int c = blockIdx.x;
   const int64_t row = blockIdx.y;  // t * M + i
   const int t = (int)(row / a.M), i = (int)(row % a.M);
-  const uint16_t* base = reinterpret_cast<const uint16_t*>(a.logits) + (int64_t)t * a.l_st + (int64_t)i * a.l_sm;
   const int64_t lo = (int64_t)c * a.chunk;
+  const uint16_t* rb = reinterpret_cast<const uint16_t*>(a.logits) + (int64_t)t * a.l_st + (int64_t)i * a.l_sm + lo;
   const int n = (int)(min(lo + a.chunk, a.V) - lo);
   const int nvec = n >> 3;
+  const int nsub = (nvec + kSubVec - 1) / kSubVec;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   __shared__ uint32_t red_u[kNw];
-  __shared__ float red_l[kNw], red_s[kNw];
+  __shared__ int red_i[kNw], red_n[kNw];
+  __shared__ float red_m[kNw], red_l[kNw], red_s[kNw];
 
-  // Vector v of this thread covers chunk elements [8 * (tid + 256 v), +8);
-  // vectors past the chunk hold -inf (they come after every real element).
+  // Vector v of sub-tile s of this thread: range vector s*kSubVec + tid + kStrThreads*v.
+  // Vectors past the range hold -inf (they come after every real element);
+  // their loads re-read the last vector, so that every load is unconditional
+  // and the loads of the next sub-tile stay in flight (counted waits).
   const uint32_t pad = kNegInfBits | (kNegInfBits << 16);
-  u32x4 raw[kVecPerThread];
+  auto load = [&](int s, u32x4 (&r)[kStrVec]) {
 #pragma unroll
-  for (int v = 0; v < kVecPerThread; ++v) {
-    const int vi = tid + kRowThreads * v;
-    raw[v] = vi < nvec ? *reinterpret_cast<const u32x4*>(base + lo + 8 * vi) : u32x4{pad, pad, pad, pad};
+    for (int v = 0; v < kStrVec; ++v) {
+      const int vi = s * kSubVec + tid + kStrThreads * v;
+      r[v] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(rb) + min(vi, nvec - 1));
+    }
+  };
+  auto pad_tail = [&](int s, u32x4 (&r)[kStrVec]) {
+#pragma unroll
+    for (int v = 0; v < kStrVec; ++v)
+      if (s * kSubVec + tid + kStrThreads * v >= nvec) r[v] = u32x4{pad, pad, pad, pad};
+  };
+
+  uint32_t bk = 0;          // largest key seen (0: none; no number has key 0)
+  int bs = -1;              // the sub-tile where it first occurred
+  int nan_i = 0x7fffffff;   // first NaN index in the range
+  float m = kNegInf, l = 0.f, sx = 0.f;
+  const float zs = a.inv_temp * kLog2e;
+
+  auto reduce_sub = [&](int s, u32x4 (&r)[kStrVec]) {
+    if (s == nsub - 1) pad_tail(s, r);
+    if (nan_i != 0x7fffffff) return;  // this thread's result is already NaN
+    uint32_t amax = 0, km = 0;
+#pragma unroll
+    for (int v = 0; v < kStrVec; ++v)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        amax = pk_max(amax, r[v][w] & 0x7FFF7FFFu);
+        km = pk_max(km, key2(r[v][w]));
+      }
+    amax = max(amax & 0xFFFFu, amax >> 16);
+    if (amax > kNanAbove) {  // rare: locate the first NaN
+#pragma unroll
+      for (int v = 0; v < kStrVec; ++v) {
+        const int vi = s * kSubVec + tid + kStrThreads * v;
+        for (int w = 0; w < 8 && nan_i == 0x7fffffff; ++w)
+          if (vi < nvec && ((r[v][w >> 1] >> (16 * (w & 1))) & 0x7FFFu) > kNanAbove) nan_i = 8 * vi + w;
+      }
+      return;
+    }
+    km = max(km & 0xFFFFu, km >> 16);
+    if (km > bk) {  // a larger maximum; its index is located at the end
+      bk = km;
+      bs = s;
+    }
+    if constexpr (TYPICAL) {
+      const float mt = half_to_f<F16>(key_to_bits(km)) * zs;
+      if (mt > m) {
+        const float sc = __builtin_amdgcn_exp2f(m - mt);  // m = -inf: 0
+        l *= sc;
+        sx *= sc;
+        m = mt;
+      }
+      if (m != kNegInf) {
+        float la = 0.f;
+#pragma unroll
+        for (int v = 0; v < kStrVec; ++v)
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const uint32_t cw = pk_min(r[v][w], kLowest2);  // -inf -> lowest finite (bits order = value order for < 0)
+            const float x0 = half_to_f<F16>(cw & 0xFFFFu), x1 = half_to_f<F16>(cw >> 16);
+            const float p0 = __builtin_amdgcn_exp2f(fmaf(x0, zs, -m));
+            const float p1 = __builtin_amdgcn_exp2f(fmaf(x1, zs, -m));
+            la += p0 + p1;
+            sx = fmaf(x0, p0, fmaf(x1, p1, sx));
+          }
+        l += la;
+      }
+    }
+  };
+
+  // Software pipeline: the loads of sub-tile s+1 are issued before sub-tile s
+  // is reduced.  They are issued on every iteration (the last one re-reads
+  // the last sub-tile) so that the wait counts are the same on every path.
+  if (nsub > 0) {
+    u32x4 cur[kStrVec], nxt[kStrVec];
+    load(0, cur);
+#pragma unroll 2
+    for (int s = 0; s < nsub; ++s) {
+      load(min(s + 1, nsub - 1), nxt);
+      reduce_sub(s, cur);
+#pragma unroll
+      for (int v = 0; v < kStrVec; ++v) cur[v] = nxt[v];
+    }
   }
-  // Elements past the last whole vector (n % 8 of them), one per thread.
+  // Elements past the last whole vector (n % 8 of them), one per thread; they
+  // follow every vector element of the range.
   const int ntail = n - 8 * nvec;
-  uint32_t tail_bits = kNegInfBits;
-  if (tid < ntail) tail_bits = base[lo + 8 * nvec + tid];
-
-  // NaN anywhere in the chunk?
-  uint32_t amax = tail_bits & 0x7FFFu;
-#pragma unroll
-  for (int v = 0; v < kVecPerThread; ++v)
-#pragma unroll
-    for (int w = 0; w < 4; ++w) amax = pk_max(amax, raw[v][w] & 0x7FFF7FFFu);
-  amax = max(amax & 0xFFFFu, amax >> 16);
-  const bool chunk_nan = __syncthreads_or(amax > kNanAbove) != 0;
-
-  // Largest key.
-  uint32_t kbest = 0;
-  if (!chunk_nan) {
-#pragma unroll
-    for (int v = 0; v < kVecPerThread; ++v)
-#pragma unroll
-      for (int w = 0; w < 4; ++w) kbest = pk_max(kbest, key2(raw[v][w]));
-    kbest = max(kbest & 0xFFFFu, kbest >> 16);
-    kbest = max(kbest, key2(tail_bits) & 0xFFFFu);
-  } else {
-    // Exact path: NaN halves take the largest key.
-    auto nkey = [&](uint32_t h) { return (h & 0x7FFFu) > kNanAbove ? 0xFFFFu : (key2(h) & 0xFFFFu); };
-#pragma unroll
-    for (int v = 0; v < kVecPerThread; ++v)
-#pragma unroll
-      for (int w = 0; w < 4; ++w) kbest = max(kbest, max(nkey(raw[v][w] & 0xFFFFu), nkey(raw[v][w] >> 16)));
-    kbest = max(kbest, nkey(tail_bits));
+  if (tid < ntail && nan_i == 0x7fffffff) {
+    const uint32_t h = rb[8 * nvec + tid];
+    const int idx = 8 * nvec + tid;
+    if ((h & 0x7FFFu) > kNanAbove) {
+      nan_i = idx;
+    } else {
+      const uint32_t k = key2(h) & 0xFFFFu;
+      if (k > bk) {
+        bk = k;
+        bs = nsub;  // the tail, past every sub-tile
+      }
+      if constexpr (TYPICAL) {
+        const float mt = half_to_f<F16>(h) * zs;
+        if (mt > m) {
+          const float sc = __builtin_amdgcn_exp2f(m - mt);
+          l *= sc;
+          sx *= sc;
+          m = mt;
+        }
+        if (m != kNegInf) {
+          const float x = half_to_f<F16>(pk_min(h, kLowest2) & 0xFFFFu);
+          const float p = __builtin_amdgcn_exp2f(fmaf(x, zs, -m));
+          l += p;
+          sx = fmaf(x, p, sx);
+        }
+      }
+    }
   }
+
+  // ---- workgroup reduction ---------------------------------------------------
+  // NaN: first NaN index.  Else: largest key, then its first index.
+  int nmin = nan_i;
+  uint32_t kmax = bk;
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) kbest = max(kbest, (uint32_t)__shfl_xor((int)kbest, o));
-  if (lane == 0) red_u[wv] = kbest;
+  for (int o = 32; o > 0; o >>= 1) {
+    nmin = min(nmin, __shfl_xor(nmin, o));
+    kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, o));
+  }
+  if (lane == 0) {
+    red_n[wv] = nmin;
+    red_u[wv] = kmax;
+  }
   __syncthreads();
+  int nanf = red_n[0];
   uint32_t kstar = red_u[0];
 #pragma unroll
-  for (int x = 1; x < kNw; ++x) kstar = max(kstar, red_u[x]);
-  __syncthreads();
-
-  // A zero maximum: -0 and +0 compare equal (keys 0x7FFF and 0x8000), so
-  // both count as hits and the exact scan runs.
-  const bool zmax = !chunk_nan && (kstar == 0x7FFFu || kstar == 0x8000u);
-  if (zmax) kstar = 0x8000u;
-
-  // First index holding kstar.
-  int first = 0x7fffffff;
-  {
-    auto hkey = [&](uint32_t h) {
-      const uint32_t k = chunk_nan && (h & 0x7FFFu) > kNanAbove ? 0xFFFFu : (key2(h) & 0xFFFFu);
-      return (zmax && k == 0x7FFFu) ? 0x8000u : k;
-    };
-    bool hit;
-    if (!chunk_nan && !zmax) {
-      const uint32_t kk = kstar | (kstar << 16);
-      uint32_t accz = 0x00010001u;
-#pragma unroll
-      for (int v = 0; v < kVecPerThread; ++v)
-#pragma unroll
-        for (int w = 0; w < 4; ++w) accz &= pk_min(key2(raw[v][w]) ^ kk, 0x00010001u);
-      hit = accz != 0x00010001u;
+  for (int x = 1; x < kNw; ++x) {
+    nanf = min(nanf, red_n[x]);
+    kstar = max(kstar, red_u[x]);
+  }
+  const bool has_nan = nanf != 0x7fffffff;
+  int f = 0x7fffffff;
+  if (!has_nan && bk == kstar && bs >= 0) {
+    // This thread holds the maximum: its first index, from the sub-tile where
+    // the thread's maximum first occurred (re-read; rare).
+    if (bs == nsub) {
+      f = 8 * nvec + tid;
     } else {
-      hit = true;
-    }
-    if (hit) {
-      for (int v = 0; v < kVecPerThread && first == 0x7fffffff; ++v) {
-        const int vi = tid + kRowThreads * v;
+      for (int v = 0; v < kStrVec && f == 0x7fffffff; ++v) {
+        const int vi = bs * kSubVec + tid + kStrThreads * v;
         if (vi >= nvec) break;
-        for (int w = 0; w < 8; ++w) {
-          const uint32_t h = (raw[v][w >> 1] >> (16 * (w & 1))) & 0xFFFFu;
-          if (hkey(h) == kstar) {
-            first = 8 * vi + w;
+        const u32x4 r = reinterpret_cast<const u32x4*>(rb)[vi];
+        for (int w = 0; w < 8; ++w)
+          if ((key2((r[w >> 1] >> (16 * (w & 1))) & 0xFFFFu) & 0xFFFFu) == kstar) {
+            f = 8 * vi + w;
             break;
           }
-        }
       }
     }
-    if (first == 0x7fffffff && tid < ntail && hkey(tail_bits) == kstar) first = 8 * nvec + tid;
+  }
+  if (!has_nan && kstar == 0x8000u) {
+    // Maximum +0: the first zero of either sign, rescanned exactly.
+    f = 0x7fffffff;
+    for (int vi = tid; vi < nvec && f == 0x7fffffff; vi += kStrThreads) {
+      const u32x4 r = reinterpret_cast<const u32x4*>(rb)[vi];
+      for (int w = 0; w < 8; ++w)
+        if (((r[w >> 1] >> (16 * (w & 1))) & 0x7FFFu) == 0) {
+          f = 8 * vi + w;
+          break;
+        }
+    }
+    if (f == 0x7fffffff && tid < ntail && (rb[8 * nvec + tid] & 0x7FFFu) == 0) f = 8 * nvec + tid;
   }
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) first = min(first, __shfl_xor(first, o));
-  if (lane == 0) red_u[wv] = (uint32_t)first;
-  __syncthreads();
-  int fbest = (int)red_u[0];
-#pragma unroll
-  for (int x = 1; x < kNw; ++x) fbest = min(fbest, (int)red_u[x]);
-
-  const float vbest = chunk_nan && kstar == 0xFFFFu ? __builtin_nanf("") : half_to_f<F16>(key_to_bits(kstar));
-
-  // Typical statistics against m = max(x) * log2(e) / T.
-  float mz = kNegInf, lsum = 0.f, ssum = 0.f;
+  for (int o = 32; o > 0; o >>= 1) f = min(f, __shfl_xor(f, o));
+  // Typical statistics of the wave, merged against the wave maximum.
   if constexpr (TYPICAL) {
-    const float zs = a.inv_temp * kLog2e;
-    mz = vbest * zs;
-    if (mz != kNegInf) {
-      float l = 0.f, sx = 0.f;
 #pragma unroll
-      for (int v = 0; v < kVecPerThread; ++v)
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const float x0 = half_to_f<F16>(raw[v][w] & 0xFFFFu), x1 = half_to_f<F16>(raw[v][w] >> 16);
-          const float p0 = __builtin_amdgcn_exp2f(fmaf(x0, zs, -mz));
-          const float p1 = __builtin_amdgcn_exp2f(fmaf(x1, zs, -mz));
-          l += p0 + p1;
-          sx = fmaf(x0, p0, fmaf(x1, p1, sx));
-        }
-      if (tid < ntail) {
-        const float x = half_to_f<F16>(tail_bits);
-        const float p = __builtin_amdgcn_exp2f(fmaf(x, zs, -mz));
-        l += p;
-        sx = fmaf(x, p, sx);
+    for (int o = 32; o > 0; o >>= 1) {
+      const float mo = __shfl_xor(m, o), lo2 = __shfl_xor(l, o), so = __shfl_xor(sx, o);
+      const float mn = fmaxf(m, mo);
+      if (mn != kNegInf) {
+        const float fa = __builtin_amdgcn_exp2f(m - mn), fb = __builtin_amdgcn_exp2f(mo - mn);
+        l = l * fa + lo2 * fb;
+        sx = sx * fa + so * fb;
       }
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) {
-        l += __shfl_xor(l, o);
-        sx += __shfl_xor(sx, o);
-      }
-      __syncthreads();
-      if (lane == 0) {
-        red_l[wv] = l;
-        red_s[wv] = sx;
-      }
-      __syncthreads();
-      lsum = red_l[0];
-      ssum = red_s[0];
-#pragma unroll
-      for (int x = 1; x < kNw; ++x) {
-        lsum += red_l[x];
-        ssum += red_s[x];
-      }
-      ssum *= a.inv_temp;
+      m = mn;
     }
   }
+  __syncthreads();
+  if (lane == 0) {
+    red_i[wv] = f;
+    red_m[wv] = m;
+    red_l[wv] = l;
+    red_s[wv] = sx;
+  }
+  __syncthreads();
   if (tid == 0) {
+    int fbest = red_i[0];
+    float M = red_m[0], L = red_l[0], S = red_s[0];
+#pragma unroll
+    for (int x = 1; x < kNw; ++x) {
+      fbest = min(fbest, red_i[x]);
+      if constexpr (TYPICAL) {
+        const float mn = fmaxf(M, red_m[x]);
+        if (mn != kNegInf) {
+          const float fa = __builtin_amdgcn_exp2f(M - mn), fb = __builtin_amdgcn_exp2f(red_m[x] - mn);
+          L = L * fa + red_l[x] * fb;
+          S = S * fa + red_s[x] * fb;
+        }
+        M = mn;
+      }
+    }
+    const float qnan = __builtin_nanf("");
+    float vbest, mz = kNegInf, lsum = 0.f, ssum = 0.f;
+    int ibest;
+    if (has_nan) {
+      vbest = qnan;
+      ibest = nanf;
+      if constexpr (TYPICAL) mz = lsum = ssum = qnan;
+    } else {
+      vbest = half_to_f<F16>(key_to_bits(kstar));
+      ibest = fbest;
+      if constexpr (TYPICAL) {
+        mz = M;
+        if (M != kNegInf) {
+          lsum = L;
+          ssum = S * a.inv_temp;
+        }
+      }
+    }
     const int64_t o = row * a.nchunk + c;
-    a.rstat[o] = make_float4(vbest, __int_as_float((int)(lo + fbest)), mz, lsum);
+    a.rstat[o] = make_float4(vbest, __int_as_float((int)(lo + ibest)), mz, lsum);
     if constexpr (TYPICAL) a.rstat2[o] = ssum;
   }
 }
@@ -548,12 +658,12 @@ __global__ void __launch_bounds__(1024) accept_walk_kernel(const AcceptArgs a) {
 }
 
 template <bool F16>
-hipError_t launch_rowstat16(const AcceptArgs& a, hipStream_t s) {
+hipError_t launch_stream16(const AcceptArgs& a, hipStream_t s) {
   dim3 grid((unsigned)a.nchunk, (unsigned)((int64_t)a.T * a.M));
   if (a.mode == 1)
-    hipLaunchKernelGGL((accept_rowstat16_kernel<F16, true>), grid, dim3(kRowThreads), 0, s, a);
+    hipLaunchKernelGGL((accept_stream16_kernel<F16, true>), grid, dim3(kStrThreads), 0, s, a);
   else
-    hipLaunchKernelGGL((accept_rowstat16_kernel<F16, false>), grid, dim3(kRowThreads), 0, s, a);
+    hipLaunchKernelGGL((accept_stream16_kernel<F16, false>), grid, dim3(kStrThreads), 0, s, a);
   return hipGetLastError();
 }
 
@@ -574,18 +684,40 @@ size_t accept_walk_lds_bytes(int M) {
   return ((size_t)7 * M + 1) / 2 * 8 + 8 + 16 * 8 + 16 * 4 + 64;
 }
 
+// 16-bit logits with 16-byte aligned rows stream their rows in ranges of
+// whole sub-tiles, about four workgroups per CU over all rows; other logits
+// take fixed chunks of kChunkGeneric elements.
+constexpr int64_t kChunkGeneric = 16384;
+
+static bool stream16_ok(const AcceptArgs& a) {
+  return a.l_dtype != 2 && ((uintptr_t)a.logits & 15) == 0 && (a.l_st * 2) % 16 == 0 && (a.l_sm * 2) % 16 == 0;
+}
+
+void accept_chunking(AcceptArgs& a, int cus) {
+  if (stream16_ok(a)) {
+    const int64_t rows = (int64_t)a.T * a.M, nsub = (a.V + kSub - 1) / kSub;
+    const int64_t want = std::max<int64_t>(1, (4 * (int64_t)cus + rows - 1) / rows);
+    const int64_t nb = std::min(want, nsub);
+    a.chunk = ((a.V + nb - 1) / nb + kSub - 1) / kSub * kSub;
+  } else {
+    a.chunk = kChunkGeneric;
+  }
+  a.nchunk = (int)((a.V + a.chunk - 1) / a.chunk);
+}
+
+int64_t accept_max_chunks(int64_t V) { return (V + kSub - 1) / kSub; }
+
 hipError_t launch_accept(const AcceptArgs& a, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
   if (a.T <= 0 || a.M <= 0) return hipSuccess;
   hipError_t e;
   if (ev0 != nullptr && (e = hipEventRecord(ev0, s)) != hipSuccess) return e;
-  // 16-bit logits with 16-byte aligned rows and chunks take the packed-key
-  // kernel (its chunk must fit 256 threads x 8 vectors of 8 elements).
-  const bool al16 = ((uintptr_t)a.logits & 15) == 0 && (a.l_st * 2) % 16 == 0 && (a.l_sm * 2) % 16 == 0 &&
-                    (a.chunk * 2) % 16 == 0 && a.chunk <= (int64_t)kRowThreads * kVecPerThread * 8;
+  // The streaming kernel needs 16-byte aligned rows and ranges (chunks of
+  // whole sub-tiles, from accept_chunking).
+  const bool st16 = stream16_ok(a) && a.chunk % kSub == 0;
   if (a.l_dtype == 0)
-    e = al16 ? launch_rowstat16<false>(a, s) : launch_rowstat<uint16_t>(a, s);
+    e = st16 ? launch_stream16<false>(a, s) : launch_rowstat<uint16_t>(a, s);
   else if (a.l_dtype == 1)
-    e = al16 ? launch_rowstat16<true>(a, s) : launch_rowstat<_Float16>(a, s);
+    e = st16 ? launch_stream16<true>(a, s) : launch_rowstat<_Float16>(a, s);
   else
     e = launch_rowstat<float>(a, s);
   if (e != hipSuccess) return e;

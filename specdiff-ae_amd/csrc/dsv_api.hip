@@ -690,16 +690,9 @@ int dsv_tree_verify(const dsv_tensor* q, const dsv_tensor* k, const dsv_tensor* 
 // Acceptance
 // ----------------------------------------------------------------------------
 
-static int64_t accept_chunk(int64_t V) {
-  (void)V;
-  return 16384;
-}
-
 size_t dsv_accept_workspace_bytes(int64_t T, int64_t M, int64_t V) {
   if (T <= 0 || M <= 0 || V <= 0) return 0;
-  const int64_t ch = accept_chunk(V);
-  const int64_t nchunk = (V + ch - 1) / ch;
-  const size_t rows = (size_t)T * M * nchunk;
+  const size_t rows = (size_t)T * M * dsv::accept_max_chunks(V);
   return align_up(rows * 16, 256) + align_up(rows * 4, 256);
 }
 
@@ -753,8 +746,6 @@ int dsv_tree_accept(int mode, const dsv_tensor* logits, const dsv_tensor* draft,
   a.T = (int)T;
   a.M = (int)M;
   a.V = V;
-  a.chunk = accept_chunk(V);
-  a.nchunk = (int)((V + a.chunk - 1) / a.chunk);
   a.draft = static_cast<const int64_t*>(draft->data);
   a.d_st = draft->stride[0];
   a.d_sm = draft->stride[1];
@@ -768,6 +759,7 @@ int dsv_tree_accept(int mode, const dsv_tensor* logits, const dsv_tensor* draft,
   a.inv_temp = mode == DSV_ACCEPT_TYPICAL ? 1.f / temperature : 1.f;
   a.eps = posterior_threshold;
   a.alpha = posterior_alpha;
+  dsv::accept_chunking(a, device_cus());
   const size_t rows = (size_t)T * M * a.nchunk;
   a.rstat = static_cast<float4*>(workspace);
   a.rstat2 = reinterpret_cast<float*>(static_cast<char*>(workspace) + align_up(rows * 16, 256));

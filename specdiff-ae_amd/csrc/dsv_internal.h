@@ -133,5 +133,10 @@ int attn_rows_per_block();
 int attn_blocks_per_cu();
 hipError_t launch_merge(const MergeArgs& a, hipStream_t s);
 hipError_t launch_accept(const AcceptArgs& a, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1);
+// Vocabulary ranges of the acceptance statistics: sets a.chunk and a.nchunk
+// from the logits layout, T, M, V and the GPU's CU count.
+void accept_chunking(AcceptArgs& a, int cus);
+// Upper bound of a.nchunk for a vocabulary of V (workspace sizing).
+int64_t accept_max_chunks(int64_t V);
 
 }  // namespace dsv

@@ -61,6 +61,26 @@ def test_typical_accepts_runner_up_that_greedy_rejects(gpu):
     assert gi[0, 1] < ti[0, 1]
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_typical_entropy_with_neg_inf_logits_and_tails(gpu, dtype):
+    """-inf logits have p = 0 and add nothing to the entropy (0 log 0 = 0);
+    the vocabulary is a multiple of neither 8 nor a range.  The draft token's
+    p (~0.01) lies between alpha*exp(-H) (~1e-4) and eps (0.09), so the
+    entropy decides the test: a NaN entropy would fall back to eps and reject."""
+    V, M = 5003, 3
+    lg = torch.zeros((1, M, V))
+    lg[0, :, 100:140] = float("-inf")
+    lg[0, :, 7] = 3.9
+    lg[0, :, V - 1] = float("-inf")  # in the tail past the last 16-byte vector
+    draft = torch.tensor([[0, 7, 7]])
+    parent_ref = torch.tensor([[-1, 0]])
+    pos = torch.arange(M)
+    kw = dict(temperature=1.0, posterior_threshold=0.09, posterior_alpha=0.3)
+    info = run_and_compare(lg.to(dtype).to(gpu), draft.to(gpu), parent_ref.to(gpu), pos.to(gpu), 8,
+                           mode="typical", **kw)
+    assert info[0, 1] == 2
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 def test_logit_dtypes_and_vocab_tails(gpu, dtype):
     # vocab not a multiple of the 16-byte vector width nor of the chunk size

@@ -130,6 +130,14 @@ def test_entropy_closed_forms():
     assert abs(ent - (-(0.25 * math.log(0.25) + 0.75 * math.log(0.75)))) < 1e-12
 
 
+def test_entropy_ignores_neg_inf_logits():
+    # -inf logits have p = 0 and, by 0 log 0 = 0, leave the entropy of the rest
+    row = np.array([0.0, -np.inf, math.log(3.0), -np.inf])
+    p, ent = oacc.softmax_stats(row)
+    assert p[1] == 0 and p[3] == 0
+    assert abs(ent - (-(0.25 * math.log(0.25) + 0.75 * math.log(0.75)))) < 1e-12
+
+
 def test_typical_threshold_rules():
     # uniform over V: p = 1/V, H = log V -> threshold min(eps, alpha / V) = alpha/V < 1/V when alpha < 1
     V = 100
