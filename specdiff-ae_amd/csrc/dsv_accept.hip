@@ -512,20 +512,40 @@ __global__ void __launch_bounds__(1024) accept_walk_kernel(const AcceptArgs a) {
   if (i == 0) s_err = 0;
   __syncthreads();
 
+  // Every global load a node needs is issued up front (one round trip for
+  // the statistics, parent, draft token and position; one more for the
+  // typical test's logit, addressed by the node's own parent and token).
+  int64_t tok = 0, pv = 0, praw = -1;
   if (i < M) {
-    // 1. Combine vocab-chunk statistics of row (t, i).
+    tok = a.draft[(int64_t)t * a.d_st + (int64_t)i * a.d_sm];
+    pv = a.pos[(int64_t)t * a.pos_st + (int64_t)i * a.pos_sm];
+    if (i > 0) praw = a.parent[(int64_t)t * a.p_st + (int64_t)(i - 1) * a.p_sm];
+  }
+  if (i < M) {
+    // 1. Combine vocab-chunk statistics of row (t, i), four chunks per round trip.
     const int64_t row = (int64_t)t * M + i;
     float bv = kNegInf;
     int bi = -1;
     Soft sm{kNegInf, 0.f, 0.f};
-    for (int c = 0; c < a.nchunk; ++c) {
-      const float4 st = a.rstat[row * a.nchunk + c];
-      const int ci = __float_as_int(st.y);
-      if (ci >= 0 && (bi < 0 || am_better(st.x, ci, bv, bi))) {
-        bv = st.x;
-        bi = ci;
+    for (int c0 = 0; c0 < a.nchunk; c0 += 4) {
+      float4 st[4];
+      float s2[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int c = min(c0 + u, a.nchunk - 1);
+        st[u] = a.rstat[row * a.nchunk + c];
+        s2[u] = a.mode == 1 ? a.rstat2[row * a.nchunk + c] : 0.f;
       }
-      if (a.mode == 1) sm = soft_merge(sm, Soft{st.z, st.w, a.rstat2[row * a.nchunk + c]});
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (c0 + u >= a.nchunk) break;
+        const int ci = __float_as_int(st[u].y);
+        if (ci >= 0 && (bi < 0 || am_better(st[u].x, ci, bv, bi))) {
+          bv = st[u].x;
+          bi = ci;
+        }
+        if (a.mode == 1) sm = soft_merge(sm, Soft{st[u].z, st[u].w, s2[u]});
+      }
     }
     nxt[i] = bi;
     mz[i] = sm.m;
@@ -538,7 +558,7 @@ __global__ void __launch_bounds__(1024) accept_walk_kernel(const AcceptArgs a) {
     int pe = 0;
     if (i > 0) {
       const int k = i - 1;
-      int64_t p = a.parent[(int64_t)t * a.p_st + (int64_t)k * a.p_sm];
+      int64_t p = praw;
       if (p == k) p = -1;
       if (p < -1 || p >= M - 1) {
         atomicOr(&s_err, 1);
@@ -548,6 +568,22 @@ __global__ void __launch_bounds__(1024) accept_walk_kernel(const AcceptArgs a) {
     }
     par[i] = pe;
   }
+  // Typical: the draft token's logit under the parent's distribution.
+  float xtok = 0.f;
+  bool tok_ok = false;
+  if (i > 0 && i < M && a.mode == 1) {
+    const int p = par[i];  // written by this thread
+    tok_ok = tok >= 0 && tok < a.V;
+    if (tok_ok) {
+      const int64_t off = (int64_t)t * a.l_st + (int64_t)p * a.l_sm + tok;
+      if (a.l_dtype == 0)
+        xtok = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(a.logits)[off] << 16);
+      else if (a.l_dtype == 1)
+        xtok = (float)reinterpret_cast<const _Float16*>(a.logits)[off];
+      else
+        xtok = reinterpret_cast<const float*>(a.logits)[off];
+    }
+  }
   __syncthreads();
 
   // 3. Per-node acceptance test against the parent's distribution.
@@ -555,21 +591,12 @@ __global__ void __launch_bounds__(1024) accept_walk_kernel(const AcceptArgs a) {
     int ok = 1;
     if (i > 0) {
       const int p = par[i];
-      const int64_t tok = a.draft[(int64_t)t * a.d_st + (int64_t)i * a.d_sm];
       if (a.mode == 0) {
         ok = (tok == (int64_t)nxt[p]);
       } else {
         ok = 0;
-        if (tok >= 0 && tok < a.V && lz[p] > 0.f) {
-          const int64_t off = (int64_t)t * a.l_st + (int64_t)p * a.l_sm + tok;
-          float x;
-          if (a.l_dtype == 0)
-            x = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(a.logits)[off] << 16);
-          else if (a.l_dtype == 1)
-            x = (float)reinterpret_cast<const _Float16*>(a.logits)[off];
-          else
-            x = reinterpret_cast<const float*>(a.logits)[off];
-          const float prob = __builtin_amdgcn_exp2f(fmaf(x, a.inv_temp * kLog2e, -mz[p])) / lz[p];
+        if (tok_ok && lz[p] > 0.f) {
+          const float prob = __builtin_amdgcn_exp2f(fmaf(xtok, a.inv_temp * kLog2e, -mz[p])) / lz[p];
           const float thr = fminf(a.eps, a.alpha * __expf(-hz[p]));
           ok = prob > thr;
         }
@@ -579,17 +606,20 @@ __global__ void __launch_bounds__(1024) accept_walk_kernel(const AcceptArgs a) {
   }
   __syncthreads();
 
-  // 4. Bounded ancestor closure + masked position value.
+  // 4. Bounded ancestor closure + masked position value.  The draft tokens
+  // go to LDS for the path output: 8-byte aligned from the start of mz, over
+  // mz, lz and at most 4 bytes of hz, all read for the last time in step 3.
+  int64_t* tok_lds = smem64 + (3 * M + 1) / 2;
   int64_t val = INT64_MIN;
   int vidx = 0x7fffffff;
   if (i < M) {
+    tok_lds[i] = tok;
     int okc = okv[i];
     int node = i;
     for (int h = 0; h < a.max_hops && okc; ++h) {
       node = par[node];
       okc &= okv[node];
     }
-    const int64_t pv = a.pos[(int64_t)t * a.pos_st + (int64_t)i * a.pos_sm];
     val = okc ? pv : 0;
     vidx = i;
   }
@@ -643,7 +673,7 @@ __global__ void __launch_bounds__(1024) accept_walk_kernel(const AcceptArgs a) {
     int64_t pid = -1, tok = -1;
     if (k < len) {
       pid = path[k];
-      tok = a.draft[(int64_t)t * a.d_st + pid * a.d_sm];
+      tok = tok_lds[pid];
     }
     a.out_path[(int64_t)t * a.op_st + k] = pid;
     a.out_tok[(int64_t)t * a.ot_st + k] = tok;
