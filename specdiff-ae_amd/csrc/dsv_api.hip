@@ -152,9 +152,10 @@ Plan make_plan(int64_t B, int64_t M, int64_t H, int64_t Hk, int64_t D, int64_t n
     const int64_t s0 = std::max<int64_t>(1, avail / units);
     int64_t kps_max = 16384;
     if (page_size > 0) kps_max = std::min<int64_t>(kps_max, (int64_t)(dsv::kPageLds - 2) * page_size);
-    kps_max = std::max<int64_t>(64, kps_max / 64 * 64);
-    int64_t kps = ((n_keys + s0 - 1) / s0 + 63) / 64 * 64;
-    kps = std::min(std::max<int64_t>(kps, 64), kps_max);
+    // Whole 32-key tiles per split.
+    kps_max = std::max<int64_t>(32, kps_max / 32 * 32);
+    int64_t kps = ((n_keys + s0 - 1) / s0 + 31) / 32 * 32;
+    kps = std::min(std::max<int64_t>(kps, 32), kps_max);
     p.kps = kps;
     p.n_splits = (int)((n_keys + kps - 1) / kps);
   }
