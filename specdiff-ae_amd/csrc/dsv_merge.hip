@@ -48,7 +48,14 @@ __global__ void __launch_bounds__(256) lse_merge_kernel(const MergeArgs a) {
   constexpr int CHUNK = SG * SPL;
   const int lane = threadIdx.x & 63;
   const int tc = lane % TPR, sg = lane / TPR;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  // Dispatch ids go round-robin over the 8 XCDs; remap so that XCD x merges
+  // a contiguous eighth of the rows.  Kernel 1 hands out contiguous eighths of
+  // its (batch, KV head, split) order the same way, so the rows of a (batch,
+  // KV head) tend to be merged on the XCD whose L2 their partials went through
+  // (exactly so for 8 KV heads and batch 1).
+  const int nb = gridDim.x;
+  const int bx = ((nb & 7) == 0) ? (blockIdx.x & 7) * (nb >> 3) + (blockIdx.x >> 3) : blockIdx.x;
+  const int64_t row = (int64_t)bx * 4 + (threadIdx.x >> 6);
   const int64_t nrows = (int64_t)a.B * a.Hk * a.R;
   if (row >= nrows) return;
   const int r = (int)(row % a.R);
