@@ -153,6 +153,150 @@ def bench_verify(args, lib, ev):
     return inp, total_ms / args.steps, k1_ms, t_wall, se0.elapsed_time(se1) / args.steps
 
 
+def bench_config3(args, lib, ev):
+    """128K paged prefix, 128-node tree (depth <= 12, out-degree <= 6), query
+    rows packed in bundle order (8 bundles).  MFMA-bound: 512 flop/B."""
+    from diffspec_mi355x import workloads as wl
+    from diffspec_mi355x.core.bundle_scheduler import bundle_row_order
+    from diffspec_mi355x.runtime.tree_attention import tree_verify
+
+    N, M, H, Hk, D, layers = 131072, 128, 32, 8, 128, 3
+    inp = wl.make_tree_verify_inputs(n_prefix=N, M=M, H=H, Hk=Hk, D=D, layers=layers, device="cuda", seed=2,
+                                     tree_seed=2, max_depth=12, max_outdeg=6)
+    par = torch.tensor(inp.parent, dtype=torch.int64, device="cuda")
+    perm = torch.tensor(bundle_row_order(inp.parent, num_bundles=8), dtype=torch.int32, device="cuda")
+    pools = [(inp.kv_pages[l, 0], inp.kv_pages[l, 1]) for l in range(layers)]
+
+    def step(i, arm=None):
+        if arm is not None:
+            lib.dsv_set_timing_events(arm[0], arm[1])
+        k, v = pools[i % layers]
+        return tree_verify(inp.q, k, v, N, par, page_table=inp.page_table, row_perm=perm)
+
+    n = 20
+    for i in range(10):
+        step(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(n):
+        step(i)
+    e1.record()
+    torch.cuda.synchronize()
+    us_step = e0.elapsed_time(e1) / n * 1e3
+    evs = ev.create(2 * n)
+    for i in range(n):
+        step(i, arm=(evs[2 * i], evs[2 * i + 1]))
+    torch.cuda.synchronize()
+    k1_us = statistics.mean(ev.elapsed_ms(evs[2 * i], evs[2 * i + 1]) for i in range(n)) * 1e3
+    ev.destroy(evs)
+    nb = algorithmic_bytes(N, M, H, Hk, D)
+    flops = 4 * M * H * N * D + 4 * M * H * M * D
+    return {"workload": "tree-verify attention, N=131072, M=128 (8 bundles, row-packed), paged bf16 KV, "
+                        f"{layers} KV layers rotated", "us_per_step": round(us_step, 3),
+            "kernel1_avg_us": round(k1_us, 3), "kernel1_tflops": round(flops / (k1_us * 1e-6) / 1e12, 1),
+            "kernel1_mfma_frac": round(flops / (k1_us * 1e-6) / 2.5e15, 4),
+            "kernel1_hbm_gbs": round(nb["kernel1"] / (k1_us * 1e-6) / 1e9, 1),
+            "kernel1_hbm_frac": round(nb["kernel1"] / (k1_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "flops_dense": flops, "bytes_per_launch": nb["kernel1"]}
+
+
+def bench_config5(args, lib, ev):
+    """One verify step of a Llama-3.1-8B-shaped target (32 layers, hidden 4096,
+    32/8 heads, FFN 14336, vocab 128256, RoPE theta 5e5) over a 64-node tree
+    with a 65536-token paged prefix per layer, random N(0, 0.02) bf16 weights.
+    Per layer: RMSNorm, QKV projection, RoPE at the nodes' positions, tree K/V
+    written into the pages after the prefix, the fused tree verify (kernels 1
+    and 3), o_proj, RMSNorm, SwiGLU MLP; then the final norm, lm_head and the
+    acceptance walk (kernel 4).  Projections are torch (hipBLASLt) GEMMs; they
+    are measurement scaffolding around the hot path, not part of it."""
+    from diffspec_mi355x import workloads as wl
+    from diffspec_mi355x.draft.tree_verification import tree_accept
+    from diffspec_mi355x.runtime.tree_attention import tree_verify
+
+    L, hid, H, Hk, D, F, V, N, M = 32, 4096, 32, 8, 128, 14336, 128256, 65536, 64
+    dev = "cuda"
+    inp = wl.make_tree_verify_inputs(n_prefix=N, M=M, H=H, Hk=Hk, D=D, layers=L, device=dev, seed=5, tree_seed=5)
+    g = torch.Generator(device=dev)
+    g.manual_seed(5)
+
+    def w(*shape):
+        return (torch.randn(shape, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+
+    layers = [dict(qkv=w(hid, (H + 2 * Hk) * D), o=w(H * D, hid), gu=w(hid, 2 * F), d=w(F, hid)) for _ in range(L)]
+    lm_head = w(hid, V)
+    x0 = w(M, hid) * 50
+    par = torch.tensor(inp.parent, dtype=torch.int64, device=dev)
+    pref = torch.tensor([[p - 1 for p in inp.parent[1:]]], dtype=torch.int64, device=dev)
+    pos = torch.tensor([N + d for d in inp.depth], dtype=torch.int64, device=dev)
+    draft = torch.randint(0, V, (1, M), generator=g, device=dev)
+    # RoPE tables at the nodes' positions; tree tokens occupy logical slots [N, N+M).
+    inv = 1.0 / (5e5 ** (torch.arange(0, D, 2, device=dev, dtype=torch.float32) / D))
+    ang = pos.float()[:, None] * inv[None, :]
+    cos, sin = torch.cat([ang.cos(), ang.cos()], -1)[:, None, :], torch.cat([ang.sin(), ang.sin()], -1)[:, None, :]
+    tok = torch.arange(N, N + M, device=dev)
+    phys = inp.page_table.long()[tok // inp.page_size]
+    slot = tok % inp.page_size
+
+    def rms(t):
+        tf = t.float()
+        return (tf * torch.rsqrt(tf.pow(2).mean(-1, keepdim=True) + 1e-5)).to(torch.bfloat16)
+
+    def rope(t):
+        tf = t.float()
+        rot = torch.cat([-tf[..., D // 2:], tf[..., :D // 2]], -1)
+        return (tf * cos + rot * sin).to(torch.bfloat16)
+
+    attn_events = []
+
+    def step(timed_attn=False):
+        x = x0
+        for l in range(L):
+            W = layers[l]
+            qkv = rms(x) @ W["qkv"]
+            q = rope(qkv[:, :H * D].view(M, H, D))
+            k = rope(qkv[:, H * D:(H + Hk) * D].view(M, Hk, D))
+            v = qkv[:, (H + Hk) * D:].view(M, Hk, D)
+            inp.kv_pages[l, 0][phys, :, slot, :] = k
+            inp.kv_pages[l, 1][phys, :, slot, :] = v
+            if timed_attn:
+                e = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                e[0].record()
+            o, _ = tree_verify(q.unsqueeze(0), inp.kv_pages[l, 0], inp.kv_pages[l, 1], N, par,
+                               page_table=inp.page_table)
+            if timed_attn:
+                e[1].record()
+                attn_events.append(e)
+            x = x + o.view(M, H * D) @ W["o"]
+            gu = rms(x) @ W["gu"]
+            x = x + (torch.nn.functional.silu(gu[:, :F].float()) * gu[:, F:].float()).to(torch.bfloat16) @ W["d"]
+        logits = rms(x) @ lm_head
+        return tree_accept(logits.unsqueeze(0), draft, pref, pos, 10)
+
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+    n = 10
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(n):
+        r = step()
+    e1.record()
+    torch.cuda.synchronize()
+    us_step = e0.elapsed_time(e1) / n * 1e3
+    step(timed_attn=True)
+    torch.cuda.synchronize()
+    attn_us = sum(a.elapsed_time(b) for a, b in attn_events) * 1e3
+    wbytes = sum(t.numel() * 2 for W in layers for t in W.values()) + lm_head.numel() * 2
+    kvbytes = L * algorithmic_bytes(N, M, H, Hk, D)["prefix_kv"]
+    return {"workload": "Llama-3.1-8B-shaped verify step: 32 layers, 64-node tree, 65536-token paged prefix per "
+                        "layer, random bf16 weights, lm_head + greedy acceptance",
+            "us_per_step": round(us_step, 1), "attention_us_per_step": round(attn_us, 1),
+            "attention_share": round(attn_us / us_step, 3), "weight_bytes": wbytes, "kv_bytes": kvbytes,
+            "hbm_gbs": round((wbytes + kvbytes) / (us_step * 1e-6) / 1e9, 1),
+            "accept_length": int(r["info"][0, 1])}
+
+
 def bench_accept(args, lib, ev):
     from diffspec_mi355x import workloads as wl
     from diffspec_mi355x.draft.tree_verification import tree_accept
@@ -239,6 +383,8 @@ def main():
     ap.add_argument("--cpu-max-steps", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-accept", action="store_true")
+    ap.add_argument("--no-config3", action="store_true")
+    ap.add_argument("--no-config5", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy (scale reference for the FETCH_SIZE / WRITE_SIZE "
                          "counters) and exit")
@@ -299,6 +445,12 @@ def main():
                                "the dispatch latency)", "us_per_step_in_that_pass": round(ms_step_ev * 1e3, 3)},
         "wall_s_timed": round(t_wall, 4),
     }
+    if not args.no_config3:
+        print("[bench] config 3 (N=131072, M=128)", file=sys.stderr, flush=True)
+        line["config3"] = bench_config3(args, lib, ev)
+    if not args.no_config5:
+        print("[bench] config 5 (32-layer verify step)", file=sys.stderr, flush=True)
+        line["config5"] = bench_config5(args, lib, ev)
     if not args.no_accept:
         print("[bench] acceptance kernel", file=sys.stderr, flush=True)
         line["acceptance"] = bench_accept(args, lib, ev)
