@@ -530,19 +530,18 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) kf[ks] = *reinterpret_cast<const u32x4*>(kt + koff[ks]);
   };
-  auto read_v = [&](auto stage_c, u32x4 (&vf)[2][DT]) {
+  // V^T operands of half hh (keys 16*hh .. 16*hh+15) of a tile.
+  auto read_vh = [&](auto stage_c, int hh, u32x4 (&vf)[2][DT]) {
     constexpr int stage = decltype(stage_c)::value;
     const uint8_t* vt = smem + (stage * 2 + 1) * G::TILE;
 #pragma unroll
-    for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const uint8_t* p = vt + voff[dt] + hh * 16 * (2 * D);
-        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p);
-        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p + 8 * (2 * D)));
-        const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
-        vf[hh][dt] = u32x4{l2[0], l2[1], h2[0], h2[1]};
-      }
+    for (int dt = 0; dt < DT; ++dt) {
+      const uint8_t* p = vt + voff[dt] + hh * 16 * (2 * D);
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p);
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p + 8 * (2 * D)));
+      const u32x2 l2 = __builtin_bit_cast(u32x2, lo), h2 = __builtin_bit_cast(u32x2, hi);
+      vf[hh][dt] = u32x4{l2[0], l2[1], h2[0], h2[1]};
+    }
   };
 
   // Tile k in ring stage S (k & 3 == S).
@@ -554,8 +553,9 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
     if (wave_active) {
       // Operands of X_k, read now so that their latency hides behind Y_k
       // (past the last tile K(k+1) is a stale stage whose product is unused).
+      // The V^T reads are spread over the two halves of the exponentials so
+      // that the LDS burst after the barrier is shorter.
       read_k(IC<(S + 1) & 3>{}, kf);
-      read_v(IC<S>{}, vf);
 
       // ---- Y_k: online softmax of S(k) (log2 domain, lazy rescale) ----------
       if (is_tree || DMASK || k >= nfull) mask_scores(s_cur, k);
@@ -572,6 +572,9 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
       float ls = lsum;
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
+        __builtin_amdgcn_sched_barrier(0);
+        read_vh(IC<S>{}, hh, vf);
+        __builtin_amdgcn_sched_barrier(0);
         uint32_t w4[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
