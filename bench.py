@@ -287,6 +287,7 @@ def bench_config5(args, lib, ev):
     step(timed_attn=True)
     torch.cuda.synchronize()
     attn_us = sum(a.elapsed_time(b) for a, b in attn_events) * 1e3
+    commit = bench_commit(inp, N, M, L, Hk, D, n)
     wbytes = sum(t.numel() * 2 for W in layers for t in W.values()) + lm_head.numel() * 2
     kvbytes = L * algorithmic_bytes(N, M, H, Hk, D)["prefix_kv"]
     return {"workload": "Llama-3.1-8B-shaped verify step: 32 layers, 64-node tree, 65536-token paged prefix per "
@@ -294,7 +295,53 @@ def bench_config5(args, lib, ev):
             "us_per_step": round(us_step, 1), "attention_us_per_step": round(attn_us, 1),
             "attention_share": round(attn_us / us_step, 3), "weight_bytes": wbytes, "kv_bytes": kvbytes,
             "hbm_gbs": round((wbytes + kvbytes) / (us_step * 1e-6) / 1e9, 1),
-            "accept_length": int(r["info"][0, 1])}
+            "accept_length": int(r["info"][0, 1]), "kv_commit": commit}
+
+
+def bench_commit(inp, N, M, L, Hk, D, n):
+    """Accepted-path KV commit over all 32 layers of the page pool, path of 9
+    nodes (depth 8) from device memory, against the reference's op sequence
+    (per layer and K/V cache: gather of the selected rows, copy to the front;
+    draft/tree_verification.py:197-217) on dense caches of the same rows."""
+    from diffspec_mi355x.draft.tree_verification import kv_commit
+
+    path_nodes = [0, 1, 3, 7, 12, 20, 33, 47, 60]
+    path = torch.full((1, M), -1, dtype=torch.int64, device="cuda")
+    path[0, :len(path_nodes)] = torch.tensor(path_nodes, device="cuda")
+    info = torch.tensor([[path_nodes[-1], len(path_nodes) - 1, 0, len(path_nodes)]], dtype=torch.int64, device="cuda")
+    for _ in range(5):
+        kv_commit(inp.kv_pages, N, path, info, page_table=inp.page_table)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(n):
+        kv_commit(inp.kv_pages, N, path, info, page_table=inp.page_table)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) / n * 1e3
+    # The reference's sequence on dense per-layer caches [2, 1, Hk, S, D]
+    # holding the same rows (S = the tree's slots plus a prefix tail).
+    S, start = 1024, 1024 - M
+    dense = [torch.randn((2, 1, Hk, S, D), device="cuda").to(torch.bfloat16) for _ in range(L)]
+    sel = torch.tensor(path_nodes, dtype=torch.long, device="cuda") + start
+
+    def ref():
+        for data in dense:
+            tgt = data[..., sel, :]
+            data[..., start:start + sel.numel(), :].copy_(tgt, non_blocking=True)
+
+    for _ in range(3):
+        ref()
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(n):
+        ref()
+    e1.record()
+    torch.cuda.synchronize()
+    us_ref = e0.elapsed_time(e1) / n * 1e3
+    moved = 2 * L * 2 * Hk * len(path_nodes) * D * 2
+    return {"layers": L, "path_nodes": len(path_nodes), "bytes_moved": moved, "us": round(us, 2),
+            "reference_ops_us": round(us_ref, 1), "reference_ops_launches": 2 * L}
 
 
 def bench_accept(args, lib, ev):

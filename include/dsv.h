@@ -224,6 +224,33 @@ int dsv_tree_accept(int mode, const dsv_tensor* logits, const dsv_tensor* draft,
                     dsv_tensor* out_info, dsv_tensor* out_next,
                     void* workspace, size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------------- */
+/* Accepted-path KV commit                                                    */
+/* ------------------------------------------------------------------------- */
+
+/*
+ * KV compaction after the walk — draft/tree_verification.py:197-217
+ * (select_indices = path + start; data[..., start:start+n, :] =
+ * data[..., select_indices, :] for every cache tensor; cache length =
+ * start + n).  One launch for every row of the cache; the path and its
+ * length n are read from device memory (the outputs of dsv_tree_accept),
+ * so no host round trip is needed.  Every read happens before any write,
+ * as with the reference's gather into a temporary.
+ *   kv          page pool [L, 2, P, Hk, page, D] with page_table, or, when
+ *               page_table has ndim 0, a dense cache [..., S, D] with 1..4
+ *               leading dimensions; bf16|f16|f32, innermost stride 1,
+ *               16-byte aligned token rows
+ *   page_table  [n_logical] int32|int64 (logical page -> physical page)
+ *   start       first tree token (cache length - M)
+ *   path        [M] or [T, M] int64: accepted node ids, root first
+ *   info        [4] or [T, 4] int64: info[3] = path length n
+ *   tree        which tree of path / info (0 for one tree)
+ * The cache length itself (start + n) is the caller's.
+ */
+int dsv_kv_commit(const dsv_tensor* kv, const dsv_tensor* page_table, int64_t start,
+                  const dsv_tensor* path, const dsv_tensor* info, int64_t tree,
+                  void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -11,6 +11,9 @@ with p_T = softmax(logits / T) and H its exact entropy (0 log 0 = 0); the
 reference has no typical mode, so this function defines it.
 ``brute_force_greedy`` is an independent formulation used to pin
 ``greedy_walk``: a node is accepted iff every edge on its root path matches.
+``kv_commit`` restates the KV compaction after the walk
+(draft/tree_verification.py:197-217): a gather of the accepted rows into a
+temporary, then a copy to the front of the tree's slots.
 """
 
 from __future__ import annotations
@@ -121,3 +124,14 @@ def brute_force_greedy(logits: np.ndarray, draft: Sequence[int], parent: Sequenc
         node = parent[node] if node != 0 else -1
     path.reverse()
     return path, len(path) - 1, int(nxt[best])
+
+
+def kv_commit(cache: np.ndarray, start: int, path: Sequence[int]) -> np.ndarray:
+    """draft/tree_verification.py:197-217 on one cache tensor [..., S, D]:
+    select_indices = path + start; tgt = data[..., select_indices, :] (a new
+    array); data[..., start:start + len(path), :] = tgt.  Returns a copy."""
+    out = np.array(cache, copy=True)
+    sel = np.asarray(path, dtype=np.int64) + int(start)
+    tgt = out[..., sel, :].copy()
+    out[..., int(start):int(start) + sel.size, :] = tgt
+    return out

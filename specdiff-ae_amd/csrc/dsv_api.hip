@@ -697,6 +697,88 @@ size_t dsv_accept_workspace_bytes(int64_t T, int64_t M, int64_t V) {
   return align_up(rows * 16, 256) + align_up(rows * 4, 256);
 }
 
+int dsv_kv_commit(const dsv_tensor* kv, const dsv_tensor* page_table, int64_t start, const dsv_tensor* path,
+                  const dsv_tensor* info, int64_t tree, void* stream) {
+  int rc;
+  if (kv == nullptr || kv->ndim < 2 || kv->ndim > 6) return fail(DSV_ERR_INVALID, "kv must have 2..6 dimensions");
+  if ((rc = check_nd(kv, "kv", kv->ndim)) != DSV_OK) return rc;
+  if (kv->dtype != DSV_BF16 && kv->dtype != DSV_F16 && kv->dtype != DSV_F32)
+    return fail(DSV_ERR_INVALID, "kv must be bf16, f16 or f32");
+  const int nd = kv->ndim;
+  const int esize = kv->dtype == DSV_F32 ? 4 : 2;
+  if (kv->stride[nd - 1] != 1) return fail(DSV_ERR_INVALID, "kv innermost stride must be 1");
+  const int64_t D = kv->shape[nd - 1];
+  if ((D * esize) % 16 != 0) return fail(DSV_ERR_UNSUPPORTED, "token rows must be a multiple of 16 bytes");
+  if ((reinterpret_cast<uintptr_t>(kv->data) & 15) != 0) return fail(DSV_ERR_INVALID, "kv must be 16-byte aligned");
+  for (int d = 0; d < nd - 1; ++d)
+    if ((kv->stride[d] * esize) % 16 != 0) return fail(DSV_ERR_INVALID, "kv strides must keep token rows 16-byte aligned");
+  if (path == nullptr || (path->ndim != 1 && path->ndim != 2)) return fail(DSV_ERR_INVALID, "path must be [M] or [T, M]");
+  if ((rc = check_nd(path, "path", path->ndim)) != DSV_OK) return rc;
+  if (info == nullptr || (info->ndim != 1 && info->ndim != 2)) return fail(DSV_ERR_INVALID, "info must be [4] or [T, 4]");
+  if ((rc = check_nd(info, "info", info->ndim)) != DSV_OK) return rc;
+  if (path->dtype != DSV_I64 || info->dtype != DSV_I64) return fail(DSV_ERR_INVALID, "path and info must be int64");
+  if (path->stride[path->ndim - 1] != 1 || info->stride[info->ndim - 1] != 1)
+    return fail(DSV_ERR_INVALID, "path and info innermost stride must be 1");
+  if (info->shape[info->ndim - 1] < 4) return fail(DSV_ERR_INVALID, "info rows must hold 4 entries");
+  const int64_t T = path->ndim == 2 ? path->shape[0] : 1;
+  if ((info->ndim == 2 ? info->shape[0] : 1) != T) return fail(DSV_ERR_INVALID, "path and info must hold the same trees");
+  if (tree < 0 || tree >= T) return fail(DSV_ERR_INVALID, "tree %lld out of range", (long long)tree);
+  const int64_t M = path->shape[path->ndim - 1];
+  if (M < 1) return fail(DSV_ERR_INVALID, "path must hold at least one node");
+  if (M * (D * esize / 16) > (int64_t)dsv::kCommitThreads * dsv::kCommitChunks)
+    return fail(DSV_ERR_UNSUPPORTED, "M * row bytes above %d KiB", dsv::kCommitThreads * dsv::kCommitChunks / 64);
+  if (start < 0) return fail(DSV_ERR_INVALID, "start must be >= 0");
+
+  dsv::CommitArgs c{};
+  c.data = kv->data;
+  c.esize = esize;
+  c.D = (int)D;
+  c.start = start;
+  c.M = (int)M;
+  c.path = static_cast<const int64_t*>(path->data) + (path->ndim == 2 ? tree * path->stride[0] : 0);
+  c.info = static_cast<const int64_t*>(info->data) + (info->ndim == 2 ? tree * info->stride[0] : 0);
+  if (present(page_table)) {
+    if (nd != 6) return fail(DSV_ERR_INVALID, "a paged kv must be [L, 2, P, Hk, page, D]");
+    if ((rc = check_nd(page_table, "page_table", 1)) != DSV_OK) return rc;
+    if (page_table->dtype != DSV_I32 && page_table->dtype != DSV_I64)
+      return fail(DSV_ERR_INVALID, "page_table must be int32 or int64");
+    if (page_table->stride[0] != 1) return fail(DSV_ERR_INVALID, "page_table stride must be 1");
+    const int sh = log2_exact(kv->shape[4]);
+    if (sh < 0) return fail(DSV_ERR_UNSUPPORTED, "page size must be a power of two");
+    if (start + M > page_table->shape[0] * kv->shape[4])
+      return fail(DSV_ERR_INVALID, "tokens [start, start + M) exceed the page table");
+    c.nlead = 3;
+    const int lead[3] = {0, 1, 3};
+    c.rows = 1;
+    for (int x = 0; x < 3; ++x) {
+      c.lead_shape[x] = kv->shape[lead[x]];
+      c.lead_stride[x] = kv->stride[lead[x]];
+      c.rows *= kv->shape[lead[x]];
+    }
+    c.pt = page_table->data;
+    c.pt_i64 = page_table->dtype == DSV_I64;
+    c.ps_shift = sh;
+    c.page_stride = kv->stride[2];
+    c.n_phys = kv->shape[2];
+    c.tok_stride = kv->stride[4];
+  } else {
+    if (nd < 3) return fail(DSV_ERR_INVALID, "a dense kv must be [..., S, D] with at least one leading dimension");
+    if (start + M > kv->shape[nd - 2]) return fail(DSV_ERR_INVALID, "tokens [start, start + M) exceed the cache");
+    c.nlead = nd - 2;
+    c.rows = 1;
+    for (int x = 0; x < nd - 2; ++x) {
+      c.lead_shape[x] = kv->shape[x];
+      c.lead_stride[x] = kv->stride[x];
+      c.rows *= kv->shape[x];
+    }
+    c.tok_stride = kv->stride[nd - 2];
+  }
+  if (g_dry_run) return DSV_OK;
+  const hipError_t e = dsv::launch_commit(c, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "kv commit launch");
+  return DSV_OK;
+}
+
 int dsv_tree_accept(int mode, const dsv_tensor* logits, const dsv_tensor* draft, const dsv_tensor* parent,
                     const dsv_tensor* pos, int64_t max_hops, float temperature, float posterior_threshold,
                     float posterior_alpha, dsv_tensor* out_path, dsv_tensor* out_tokens, dsv_tensor* out_info,

@@ -124,6 +124,27 @@ struct AcceptArgs {
   int64_t* out_next; int64_t on_st;
 };
 
+// Arguments of the accepted-path KV commit.
+constexpr int kCommitThreads = 256;
+constexpr int kCommitChunks = 16;          // 16-byte chunks per thread: n * D * esize <= 64 KiB
+struct CommitArgs {
+  void* data;                // cache base (bf16/f16: esize 2, f32: esize 4)
+  int esize;
+  int64_t rows;              // cache rows moved independently
+  int nlead;                 // leading dimensions decomposing a row index (<= 4)
+  int64_t lead_shape[4], lead_stride[4];
+  int64_t tok_stride;        // elements between tokens (within a page when paged)
+  const void* pt;            // page table (nullptr: dense)
+  int pt_i64;
+  int ps_shift;
+  int64_t page_stride, n_phys;
+  int D;                     // elements per token row (innermost stride 1)
+  int64_t start;             // first tree token
+  int M;                     // tree nodes
+  const int64_t* path;       // [M] accepted node ids (root first)
+  const int64_t* info;       // info[3] = path length
+};
+
 // ---------------------------------------------------------------------------
 // Launchers (defined in the .hip files, called by the C-ABI layer).
 // ---------------------------------------------------------------------------
@@ -133,6 +154,7 @@ int attn_rows_per_block();
 int attn_blocks_per_cu();
 hipError_t launch_merge(const MergeArgs& a, hipStream_t s);
 hipError_t launch_accept(const AcceptArgs& a, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1);
+hipError_t launch_commit(const CommitArgs& a, hipStream_t s);
 // Vocabulary ranges of the acceptance statistics: sets a.chunk and a.nchunk
 // from the logits layout, T, M, V and the GPU's CU count.
 void accept_chunking(AcceptArgs& a, int cus);

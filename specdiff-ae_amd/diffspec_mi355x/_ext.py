@@ -69,6 +69,7 @@ SIGNATURES = {
         [ctypes.c_int, _P, _P, _P, _P, _I64, ctypes.c_float, ctypes.c_float, ctypes.c_float, _P, _P, _P, _P, _V,
          _SZ, _V],
     ),
+    "dsv_kv_commit": (ctypes.c_int, [_P, _P, _I64, _P, _P, _I64, _V]),
 }
 
 _lib: Optional[ctypes.CDLL] = None

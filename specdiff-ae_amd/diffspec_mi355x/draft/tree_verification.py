@@ -28,7 +28,7 @@ import torch
 from .. import _ext
 from ..core.bundle_scheduler import BundleScheduler
 
-__all__ = ["tree_accept", "evaluate_tree", "verify", "verify_new"]
+__all__ = ["tree_accept", "evaluate_tree", "kv_commit", "verify", "verify_new"]
 
 
 def tree_accept(logits: torch.Tensor, draft: torch.Tensor, parent: torch.Tensor, pos: torch.Tensor,
@@ -81,15 +81,36 @@ def tree_accept(logits: torch.Tensor, draft: torch.Tensor, parent: torch.Tensor,
     return out
 
 
-def evaluate_tree(logits: torch.Tensor, draft: torch.Tensor, parent: torch.Tensor, position_ids: torch.Tensor,
-                  max_depth: int, mode: str = "greedy", temperature: float = 1.0,
-                  posterior_threshold: float = 0.09,
-                  posterior_alpha: float = 0.3) -> Tuple[list, list, int, torch.Tensor, int]:
-    """Lines :100-182 of verify_new for one tree.
+def kv_commit(kv: torch.Tensor, start: int, path: torch.Tensor, info: torch.Tensor,
+              page_table: Optional[torch.Tensor] = None, tree: int = 0) -> None:
+    """Accepted-path KV commit on the GPU (reference draft/tree_verification.py:197-217).
 
-    Returns (best_candidate tokens, best_candidate node ids, accept_length,
-    next_token [1, 1] on the device, max_id).
+    Tokens [start, start + n) of every row of ``kv`` receive tokens
+    start + path[0..n), n = info[3], every read before any write (the
+    reference's ``data[..., start:start+n, :] = data[..., start + path, :]``).
+    ``path`` / ``info`` are the device outputs of :func:`tree_accept`
+    (``[T, M]`` / ``[T, 4]``, or one tree's rows), so no host round trip is
+    needed.  ``kv`` is a page pool ``[L, 2, P, Hk, page, D]`` with
+    ``page_table``, or a dense cache ``[..., S, D]`` (1..4 leading dims);
+    bf16/f16/f32 with 16-byte token rows.
     """
+    _ext.require_gpu(kv, path, info)
+    lib = _ext.load()
+    rc = lib.dsv_kv_commit(_ext.desc(kv), _ext.desc(page_table), int(start), _ext.desc(path), _ext.desc(info),
+                           int(tree), _ext.stream_of(kv.device))
+    _ext.check(rc, "kv_commit")
+
+
+def _kv_commit_ok(t: torch.Tensor) -> bool:
+    """Whether the commit kernel takes this dense cache tensor as it is."""
+    es = t.element_size()
+    return (t.is_cuda and t.dtype in (torch.bfloat16, torch.float16, torch.float32) and 3 <= t.dim() <= 6
+            and t.stride(-1) == 1 and (t.shape[-1] * es) % 16 == 0 and t.data_ptr() % 16 == 0
+            and all((st * es) % 16 == 0 for st in t.stride()[:-1]))
+
+
+def _evaluate_tree_dev(logits, draft, parent, position_ids, max_depth, mode, temperature, posterior_threshold,
+                       posterior_alpha):
     M = draft.shape[-1]
     pos = position_ids[0] if position_ids.dim() == 2 else position_ids
     max_hops = min(int(max_depth) + 2, M)
@@ -103,7 +124,20 @@ def evaluate_tree(logits: torch.Tensor, draft: torch.Tensor, parent: torch.Tenso
     ids = host[4:4 + plen]
     toks = host[4 + M:4 + M + plen]
     next_token = r["info"][:, 2:3]
-    return toks, ids, int(accept_length), next_token, int(winner)
+    return (toks, ids, int(accept_length), next_token, int(winner)), r
+
+
+def evaluate_tree(logits: torch.Tensor, draft: torch.Tensor, parent: torch.Tensor, position_ids: torch.Tensor,
+                  max_depth: int, mode: str = "greedy", temperature: float = 1.0,
+                  posterior_threshold: float = 0.09,
+                  posterior_alpha: float = 0.3) -> Tuple[list, list, int, torch.Tensor, int]:
+    """Lines :100-182 of verify_new for one tree.
+
+    Returns (best_candidate tokens, best_candidate node ids, accept_length,
+    next_token [1, 1] on the device, max_id).
+    """
+    return _evaluate_tree_dev(logits, draft, parent, position_ids, max_depth, mode, temperature,
+                              posterior_threshold, posterior_alpha)[0]
 
 
 def verify(input_ids, logits, draft, position_ids, hidden_states, tree_attention_mask, past_key_values_data,
@@ -130,9 +164,9 @@ def verify_new(input_ids, logits, draft, position_ids, hidden_states, tree_atten
             "use acceptance='greedy' or acceptance='typical'")
 
     # 1-2. Acceptance walk on the GPU (reference :100-182).
-    best_candidate, best_candidate_id, accept_length, next_token, max_id = evaluate_tree(
-        logits, draft, parent, position_ids, max_depth, mode=acceptance, temperature=temperature,
-        posterior_threshold=posterior_threshold, posterior_alpha=posterior_alpha)
+    (best_candidate, best_candidate_id, accept_length, next_token, max_id), acc = _evaluate_tree_dev(
+        logits, draft, parent, position_ids, max_depth, acceptance, temperature, posterior_threshold,
+        posterior_alpha)
     next_token = next_token.to(draft.device)
     pos_all = position_ids[0] if position_ids.dim() == 2 else position_ids
 
@@ -177,9 +211,14 @@ def verify_new(input_ids, logits, draft, position_ids, hidden_states, tree_atten
         model.draft_model.attn_scores_final = torch.cat(
             (last_attn_scores[:prev_input_len], last_attn_scores[abs_ids]), dim=0)
     n_sel = len(best_candidate_id)
+    # Cache tensors the commit kernel takes are compacted on the GPU from the
+    # walk's device-side path; other layouts take the reference's gather + copy.
     for data in past_key_values_data:
-        tgt = data[..., select_indices.to(data.device), :]
-        data[..., start:start + n_sel, :].copy_(tgt, non_blocking=True)
+        if _kv_commit_ok(data) and start + int(draft.size(1)) <= data.shape[-2] and data.device == acc["path"].device:
+            kv_commit(data, start, acc["path"], acc["info"])
+        else:
+            tgt = data[..., select_indices.to(data.device), :]
+            data[..., start:start + n_sel, :].copy_(tgt, non_blocking=True)
     current_length_data.fill_(start + n_sel)
 
     # 4. Append the accepted path and build the next draft tree (reference :219-257).

@@ -103,6 +103,36 @@ def test_accept_validation(dsv_lib):
     assert rc == -1 and "mode" in _ext.last_error()
 
 
+def test_kv_commit_validation(dsv_lib):
+    path = _t((1, 8), _ext.DSV_I64)
+    info = _t((1, 4), _ext.DSV_I64)
+    none = _ext.DsvTensor()
+    kv_odd = _t((2, 2, 40, 6), _ext.DSV_BF16)  # 12-byte token rows
+    rc = dsv_lib.dsv_kv_commit(ctypes.byref(kv_odd), ctypes.byref(none), 10, ctypes.byref(path), ctypes.byref(info),
+                               0, None)
+    assert rc == -2 and "16 bytes" in _ext.last_error()
+    kv = _t((2, 2, 40, 64), _ext.DSV_BF16)
+    rc = dsv_lib.dsv_kv_commit(ctypes.byref(kv), ctypes.byref(none), 35, ctypes.byref(path), ctypes.byref(info),
+                               0, None)
+    assert rc == -1 and "exceed the cache" in _ext.last_error()
+    rc = dsv_lib.dsv_kv_commit(ctypes.byref(kv), ctypes.byref(none), 10, ctypes.byref(path), ctypes.byref(info),
+                               1, None)
+    assert rc == -1 and "tree" in _ext.last_error()
+    pool = _t((2, 2, 6, 2, 16, 64), _ext.DSV_BF16)
+    pt = _t((4,), _ext.DSV_I32)
+    rc = dsv_lib.dsv_kv_commit(ctypes.byref(pool), ctypes.byref(pt), 60, ctypes.byref(path), ctypes.byref(info),
+                               0, None)
+    assert rc == -1 and "page table" in _ext.last_error()
+    # A valid call plans without launching in dry-run mode.
+    dsv_lib.dsv_set_dry_run(1)
+    try:
+        rc = dsv_lib.dsv_kv_commit(ctypes.byref(pool), ctypes.byref(pt), 40, ctypes.byref(path), ctypes.byref(info),
+                                   0, None)
+    finally:
+        dsv_lib.dsv_set_dry_run(0)
+    assert rc == 0
+
+
 def test_python_api_refuses_cpu_tensors(dsv_lib):
     from diffspec_mi355x.runtime.tree_attention import prefix_attention_forward, tree_verify
     from diffspec_mi355x.draft.tree_verification import tree_accept

@@ -166,3 +166,20 @@ def test_typical_with_planted_path_equals_greedy():
     logits, draft, parent, depth, pos = planted_case(M, V, 11, plen=5)
     pref = wl.parent_to_reference(parent)
     assert oacc.typical_walk(logits, draft, pref, pos, 8)[1] == oacc.greedy_walk(logits, draft, pref, pos, 8)[1]
+
+
+def test_kv_commit_matches_row_by_row_copy_from_the_old_cache():
+    # Brute force: every destination row reads the cache as it was before the
+    # commit, including when a source slot is also a destination (path
+    # [0, 2, 3, 5]: slot 2 is read for row 1 and written by row 2).
+    rng = np.random.default_rng(3)
+    cache = rng.standard_normal((2, 3, 40, 5))
+    for path in ([0, 2, 3, 5], [0], list(range(12)), [0, 1, 7, 8, 11]):
+        got = oacc.kv_commit(cache, 20, path)
+        want = cache.copy()
+        for lead in np.ndindex(*cache.shape[:-2]):
+            for i, p in enumerate(path):
+                want[lead + (20 + i,)] = cache[lead + (20 + p,)]
+        assert np.array_equal(got, want)
+        untouched = [t for t in range(40) if not 20 <= t < 20 + len(path)]
+        assert np.array_equal(got[..., untouched, :], cache[..., untouched, :])
