@@ -201,17 +201,41 @@ def bench_config3(args, lib, ev):
             "flops_dense": flops, "bytes_per_launch": nb["kernel1"]}
 
 
+def device_us(fn, calls=10, reps=20):
+    """Device time per call of fn: `calls` calls captured once in a HIP graph,
+    replayed `reps` times (host launch cost excluded).  fn records no memset
+    nodes."""
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(calls):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / (reps * calls) * 1e3
+
+
 def bench_config5(args, lib, ev):
     """One verify step of a Llama-3.1-8B-shaped target (32 layers, hidden 4096,
     32/8 heads, FFN 14336, vocab 128256, RoPE theta 5e5) over a 64-node tree
     with a 65536-token paged prefix per layer, random N(0, 0.02) bf16 weights.
-    Per layer: RMSNorm, QKV projection, RoPE at the nodes' positions, tree K/V
-    written into the pages after the prefix, the fused tree verify (kernels 1
-    and 3), o_proj, RMSNorm, SwiGLU MLP; then the final norm, lm_head and the
-    acceptance walk (kernel 4).  Projections are torch (hipBLASLt) GEMMs; they
-    are measurement scaffolding around the hot path, not part of it."""
+    Per layer: RMSNorm, QKV projection, RoPE of q and k at the nodes'
+    positions with the tree K/V written into the pages after the prefix (one
+    dsv_kv_append launch), the fused tree verify (kernels 1 and 3), o_proj,
+    RMSNorm, SwiGLU MLP; then the final norm, lm_head and the acceptance walk
+    (kernel 4).  Projections, norms and the MLP are torch (hipBLASLt) ops:
+    measurement scaffolding around the hot path, not part of it."""
     from diffspec_mi355x import workloads as wl
     from diffspec_mi355x.draft.tree_verification import tree_accept
+    from diffspec_mi355x.runtime.cache_state import append_tree_kv
     from diffspec_mi355x.runtime.tree_attention import tree_verify
 
     L, hid, H, Hk, D, F, V, N, M = 32, 4096, 32, 8, 128, 14336, 128256, 65536, 64
@@ -233,7 +257,8 @@ def bench_config5(args, lib, ev):
     # RoPE tables at the nodes' positions; tree tokens occupy logical slots [N, N+M).
     inv = 1.0 / (5e5 ** (torch.arange(0, D, 2, device=dev, dtype=torch.float32) / D))
     ang = pos.float()[:, None] * inv[None, :]
-    cos, sin = torch.cat([ang.cos(), ang.cos()], -1)[:, None, :], torch.cat([ang.sin(), ang.sin()], -1)[:, None, :]
+    cos = torch.cat([ang.cos(), ang.cos()], -1).to(torch.bfloat16)
+    sin = torch.cat([ang.sin(), ang.sin()], -1).to(torch.bfloat16)
     tok = torch.arange(N, N + M, device=dev)
     phys = inp.page_table.long()[tok // inp.page_size]
     slot = tok % inp.page_size
@@ -242,10 +267,9 @@ def bench_config5(args, lib, ev):
         tf = t.float()
         return (tf * torch.rsqrt(tf.pow(2).mean(-1, keepdim=True) + 1e-5)).to(torch.bfloat16)
 
-    def rope(t):
-        tf = t.float()
-        rot = torch.cat([-tf[..., D // 2:], tf[..., :D // 2]], -1)
-        return (tf * cos + rot * sin).to(torch.bfloat16)
+    def rope_ref(t):  # the reference's op sequence on [M, heads, D]
+        c, s_ = cos[:, None, :], sin[:, None, :]
+        return (t * c) + (torch.cat((-t[..., D // 2:], t[..., :D // 2]), -1) * s_)
 
     attn_events = []
 
@@ -254,11 +278,9 @@ def bench_config5(args, lib, ev):
         for l in range(L):
             W = layers[l]
             qkv = rms(x) @ W["qkv"]
-            q = rope(qkv[:, :H * D].view(M, H, D))
-            k = rope(qkv[:, H * D:(H + Hk) * D].view(M, Hk, D))
-            v = qkv[:, (H + Hk) * D:].view(M, Hk, D)
-            inp.kv_pages[l, 0][phys, :, slot, :] = k
-            inp.kv_pages[l, 1][phys, :, slot, :] = v
+            q = append_tree_kv(qkv[:, H * D:(H + Hk) * D].view(M, Hk, D), qkv[:, (H + Hk) * D:].view(M, Hk, D),
+                               inp.kv_pages[l, 0], inp.kv_pages[l, 1], N, cos=cos, sin=sin,
+                               page_table=inp.page_table, q=qkv[:, :H * D].view(M, H, D))
             if timed_attn:
                 e = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                 e[0].record()
@@ -288,6 +310,24 @@ def bench_config5(args, lib, ev):
     torch.cuda.synchronize()
     attn_us = sum(a.elapsed_time(b) for a, b in attn_events) * 1e3
     commit = bench_commit(inp, N, M, L, Hk, D, n)
+    # The append alone (one layer): q/k RoPE + tree K/V into the pages, one
+    # launch, against the reference's ops (RoPE of q and k in bf16 torch ops,
+    # then the K/V writes into the pages).
+    qkv = rms(x0) @ layers[0]["qkv"]
+    qs, ks, vs = (qkv[:, :H * D].view(M, H, D), qkv[:, H * D:(H + Hk) * D].view(M, Hk, D),
+                  qkv[:, (H + Hk) * D:].view(M, Hk, D))
+
+    def ours():
+        append_tree_kv(ks, vs, inp.kv_pages[0, 0], inp.kv_pages[0, 1], N, cos=cos, sin=sin,
+                       page_table=inp.page_table, q=qs)
+
+    def theirs():
+        rope_ref(qs)
+        inp.kv_pages[0, 0][phys, :, slot, :] = rope_ref(ks)
+        inp.kv_pages[0, 1][phys, :, slot, :] = vs
+
+    app = {"us": round(device_us(ours), 2), "reference_ops_us": round(device_us(theirs), 2),
+           "timing": "device time per call, HIP graph of 10 calls replayed"}
     wbytes = sum(t.numel() * 2 for W in layers for t in W.values()) + lm_head.numel() * 2
     kvbytes = L * algorithmic_bytes(N, M, H, Hk, D)["prefix_kv"]
     return {"workload": "Llama-3.1-8B-shaped verify step: 32 layers, 64-node tree, 65536-token paged prefix per "
@@ -295,7 +335,8 @@ def bench_config5(args, lib, ev):
             "us_per_step": round(us_step, 1), "attention_us_per_step": round(attn_us, 1),
             "attention_share": round(attn_us / us_step, 3), "weight_bytes": wbytes, "kv_bytes": kvbytes,
             "hbm_gbs": round((wbytes + kvbytes) / (us_step * 1e-6) / 1e9, 1),
-            "accept_length": int(r["info"][0, 1]), "kv_commit": commit}
+            "accept_length": int(r["info"][0, 1]), "kv_commit": commit,
+            "kv_append_one_layer": dict(app, bytes=(M * (H + 2 * Hk) * D * 2) * 2)}
 
 
 def bench_commit(inp, N, M, L, Hk, D, n):
@@ -309,16 +350,7 @@ def bench_commit(inp, N, M, L, Hk, D, n):
     path = torch.full((1, M), -1, dtype=torch.int64, device="cuda")
     path[0, :len(path_nodes)] = torch.tensor(path_nodes, device="cuda")
     info = torch.tensor([[path_nodes[-1], len(path_nodes) - 1, 0, len(path_nodes)]], dtype=torch.int64, device="cuda")
-    for _ in range(5):
-        kv_commit(inp.kv_pages, N, path, info, page_table=inp.page_table)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(n):
-        kv_commit(inp.kv_pages, N, path, info, page_table=inp.page_table)
-    e1.record()
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) / n * 1e3
+    us = device_us(lambda: kv_commit(inp.kv_pages, N, path, info, page_table=inp.page_table))
     # The reference's sequence on dense per-layer caches [2, 1, Hk, S, D]
     # holding the same rows (S = the tree's slots plus a prefix tail).
     S, start = 1024, 1024 - M
@@ -330,18 +362,11 @@ def bench_commit(inp, N, M, L, Hk, D, n):
             tgt = data[..., sel, :]
             data[..., start:start + sel.numel(), :].copy_(tgt, non_blocking=True)
 
-    for _ in range(3):
-        ref()
-    torch.cuda.synchronize()
-    e0.record()
-    for _ in range(n):
-        ref()
-    e1.record()
-    torch.cuda.synchronize()
-    us_ref = e0.elapsed_time(e1) / n * 1e3
+    us_ref = device_us(ref, calls=2)
     moved = 2 * L * 2 * Hk * len(path_nodes) * D * 2
     return {"layers": L, "path_nodes": len(path_nodes), "bytes_moved": moved, "us": round(us, 2),
-            "reference_ops_us": round(us_ref, 1), "reference_ops_launches": 2 * L}
+            "reference_ops_us": round(us_ref, 1), "reference_ops_launches": 2 * L,
+            "timing": "device time per call, HIP graph replayed"}
 
 
 def bench_accept(args, lib, ev):

@@ -251,6 +251,35 @@ int dsv_kv_commit(const dsv_tensor* kv, const dsv_tensor* page_table, int64_t st
                   const dsv_tensor* path, const dsv_tensor* info, int64_t tree,
                   void* stream);
 
+/* ------------------------------------------------------------------------- */
+/* Tree K/V append with RoPE                                                  */
+/* ------------------------------------------------------------------------- */
+
+/*
+ * The tree tokens' keys and values enter the cache at logical tokens
+ * [start, start + M): keys rotated by RoPE, values as they are; queries are
+ * rotated into q_out in the same launch when given.  Replaces, per layer,
+ * apply_rotary_pos_emb_L31 (llama_target_model.py:452-473, :408-427,
+ * applied at :768-771) followed by KVCache.cat (runtime/cache_state.py:52-66,
+ * used at llama_target_model.py:781-783) or the per-token
+ * PagedKVCache.write_kv (core/kv_cache/paged_kv.py:168-223).  RoPE rounds
+ * like torch's 16-bit elementwise ops: x * cos and rotate_half(x) * sin are
+ * each rounded to the dtype, then their sum.
+ *   k, v        [M, Hk, D] or [1, M, Hk, D] bf16|f16 (projected, before RoPE)
+ *   cos, sin    [M, D] or [1, M, D] at the tree tokens' positions, same dtype
+ *               (ndim 0: no RoPE)
+ *   k_dst, v_dst  page-pool halves [P, Hk, page, D] with page_table, or
+ *               (page_table ndim 0) dense caches [Hk, S, D] or [1, Hk, S, D]
+ *   page_table  [n_logical] int32|int64
+ *   start       cache length before the tree (first tree token)
+ *   q, q_out    optional [M, H, D] or [1, M, H, D] (ndim 0 to skip)
+ * D must be a multiple of 16; token rows 16-byte aligned.
+ */
+int dsv_kv_append(const dsv_tensor* k, const dsv_tensor* v, const dsv_tensor* cos,
+                  const dsv_tensor* sin, dsv_tensor* k_dst, dsv_tensor* v_dst,
+                  const dsv_tensor* page_table, int64_t start, const dsv_tensor* q,
+                  dsv_tensor* q_out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

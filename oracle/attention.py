@@ -148,3 +148,20 @@ def bf16_round(x: np.ndarray) -> np.ndarray:
     r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
     out = (r & 0xFFFFFFFF).astype(np.uint32).view(np.float32)
     return np.where(np.isnan(a), a, out)
+
+
+def half_round(x: np.ndarray) -> np.ndarray:
+    """Round float32 values to float16 (round-to-nearest-even), returned as float32."""
+    return np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float32)
+
+
+def rope_16bit(x: np.ndarray, cos: np.ndarray, sin: np.ndarray, f16: bool = False) -> np.ndarray:
+    """x * cos + rotate_half(x) * sin as torch evaluates it on bf16/f16 tensors
+    (llama_target_model.py:408-427, 452-473): each product and the sum rounded
+    to the 16-bit dtype.  x [..., M, D] (token axis -2), cos/sin [M, D]; all
+    values already representable in the dtype."""
+    rnd = half_round if f16 else bf16_round
+    x = np.asarray(x, dtype=np.float32)
+    d = x.shape[-1] // 2
+    rot = np.concatenate([-x[..., d:], x[..., :d]], axis=-1)
+    return rnd(rnd(x * cos) + rnd(rot * sin))

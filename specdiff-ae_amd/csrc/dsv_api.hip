@@ -697,6 +697,151 @@ size_t dsv_accept_workspace_bytes(int64_t T, int64_t M, int64_t V) {
   return align_up(rows * 16, 256) + align_up(rows * 4, 256);
 }
 
+int dsv_kv_append(const dsv_tensor* k, const dsv_tensor* v, const dsv_tensor* cos, const dsv_tensor* sin,
+                  dsv_tensor* k_dst, dsv_tensor* v_dst, const dsv_tensor* page_table, int64_t start,
+                  const dsv_tensor* q, dsv_tensor* q_out, void* stream) {
+  int rc;
+  // A [lead..., X, Y, D] operand with an optional leading 1: the last three dims.
+  auto last3 = [&](const dsv_tensor* t, const char* name, int64_t s[3], int64_t st[3]) -> int {
+    int r;
+    if (t == nullptr || (t->ndim != 3 && t->ndim != 4)) return fail(DSV_ERR_INVALID, "%s must be 3-d or [1, ...] 4-d", name);
+    if ((r = check_nd(t, name, t->ndim)) != DSV_OK) return r;
+    if (t->ndim == 4 && t->shape[0] != 1) return fail(DSV_ERR_INVALID, "%s leading dimension must be 1", name);
+    const int o = t->ndim - 3;
+    for (int x = 0; x < 3; ++x) {
+      s[x] = t->shape[o + x];
+      st[x] = t->stride[o + x];
+    }
+    if (st[2] != 1) return fail(DSV_ERR_INVALID, "%s innermost stride must be 1", name);
+    if ((reinterpret_cast<uintptr_t>(t->data) & 15) != 0 || (st[0] * 2) % 16 != 0 || (st[1] * 2) % 16 != 0)
+      return fail(DSV_ERR_INVALID, "%s rows must be 16-byte aligned", name);
+    return DSV_OK;
+  };
+  int64_t ks[3], kst[3], vs[3], vst[3];
+  if ((rc = last3(k, "k", ks, kst)) != DSV_OK) return rc;
+  if ((rc = last3(v, "v", vs, vst)) != DSV_OK) return rc;
+  if (k->dtype != DSV_BF16 && k->dtype != DSV_F16) return fail(DSV_ERR_INVALID, "k must be bf16 or f16");
+  if (v->dtype != k->dtype) return fail(DSV_ERR_INVALID, "k and v must share a dtype");
+  const int64_t M = ks[0], Hk = ks[1], D = ks[2];
+  if (vs[0] != M || vs[1] != Hk || vs[2] != D) return fail(DSV_ERR_INVALID, "v must match k");
+  if (M < 1 || Hk < 1) return fail(DSV_ERR_INVALID, "empty k");
+  if (D % 16 != 0) return fail(DSV_ERR_UNSUPPORTED, "head_dim %lld must be a multiple of 16", (long long)D);
+  if (start < 0) return fail(DSV_ERR_INVALID, "start must be >= 0");
+
+  dsv::AppendArgs a{};
+  a.f16 = k->dtype == DSV_F16;
+  a.M = (int)M;
+  a.Hk = (int)Hk;
+  a.D = (int)D;
+  a.start = start;
+  a.k = static_cast<const uint16_t*>(k->data);
+  a.k_sm = kst[0];
+  a.k_sh = kst[1];
+  a.v = static_cast<const uint16_t*>(v->data);
+  a.v_sm = vst[0];
+  a.v_sh = vst[1];
+  if (present(cos) || present(sin)) {
+    if (!present(cos) || !present(sin)) return fail(DSV_ERR_INVALID, "cos and sin go together");
+    for (const dsv_tensor* t : {cos, sin}) {
+      const char* nm = t == cos ? "cos" : "sin";
+      if (t->ndim != 2 && t->ndim != 3) return fail(DSV_ERR_INVALID, "%s must be [M, D] or [1, M, D]", nm);
+      if ((rc = check_nd(t, nm, t->ndim)) != DSV_OK) return rc;
+      const int o = t->ndim - 2;
+      if ((t->ndim == 3 && t->shape[0] != 1) || t->shape[o] != M || t->shape[o + 1] != D || t->stride[o + 1] != 1)
+        return fail(DSV_ERR_INVALID, "%s must be [M, D] with innermost stride 1", nm);
+      if (t->dtype != k->dtype) return fail(DSV_ERR_INVALID, "%s must have the dtype of k", nm);
+      if ((reinterpret_cast<uintptr_t>(t->data) & 15) != 0 || (t->stride[o] * 2) % 16 != 0)
+        return fail(DSV_ERR_INVALID, "%s rows must be 16-byte aligned", nm);
+    }
+    a.cos = static_cast<const uint16_t*>(cos->data);
+    a.cs_m = cos->stride[cos->ndim - 2];
+    a.sin = static_cast<const uint16_t*>(sin->data);
+    a.sn_m = sin->stride[sin->ndim - 2];
+  }
+  if (present(q) || present(q_out)) {
+    int64_t qs[3], qst[3], os[3], ost[3];
+    if (!present(q) || !present(q_out)) return fail(DSV_ERR_INVALID, "q and q_out go together");
+    if ((rc = last3(q, "q", qs, qst)) != DSV_OK) return rc;
+    if ((rc = last3(q_out, "q_out", os, ost)) != DSV_OK) return rc;
+    if (q->dtype != k->dtype || q_out->dtype != k->dtype) return fail(DSV_ERR_INVALID, "q and q_out must have the dtype of k");
+    if (qs[0] != M || qs[2] != D || os[0] != M || os[1] != qs[1] || os[2] != D)
+      return fail(DSV_ERR_INVALID, "q and q_out must be [M, H, D]");
+    a.H = (int)qs[1];
+    a.q = static_cast<const uint16_t*>(q->data);
+    a.q_sm = qst[0];
+    a.q_sh = qst[1];
+    a.q_out = static_cast<uint16_t*>(q_out->data);
+    a.qo_sm = ost[0];
+    a.qo_sh = ost[1];
+  }
+  for (dsv_tensor* t : {k_dst, v_dst}) {
+    const char* nm = t == k_dst ? "k_dst" : "v_dst";
+    if (t == nullptr || t->data == nullptr) return fail(DSV_ERR_INVALID, "%s missing", nm);
+    if (t->dtype != k->dtype) return fail(DSV_ERR_INVALID, "%s must have the dtype of k", nm);
+    if ((reinterpret_cast<uintptr_t>(t->data) & 15) != 0) return fail(DSV_ERR_INVALID, "%s must be 16-byte aligned", nm);
+  }
+  if (present(page_table)) {
+    if ((rc = check_nd(page_table, "page_table", 1)) != DSV_OK) return rc;
+    if (page_table->dtype != DSV_I32 && page_table->dtype != DSV_I64)
+      return fail(DSV_ERR_INVALID, "page_table must be int32 or int64");
+    if (page_table->stride[0] != 1) return fail(DSV_ERR_INVALID, "page_table stride must be 1");
+    int64_t ps = 0, P = 0;
+    for (dsv_tensor* t : {k_dst, v_dst}) {
+      const char* nm = t == k_dst ? "k_dst" : "v_dst";
+      if ((rc = check_nd(t, nm, 4)) != DSV_OK) return rc;
+      if (t->shape[1] != Hk || t->shape[3] != D || t->stride[3] != 1)
+        return fail(DSV_ERR_INVALID, "%s must be [P, Hk, page, D] with innermost stride 1", nm);
+      for (int x = 0; x < 3; ++x)
+        if ((t->stride[x] * 2) % 16 != 0) return fail(DSV_ERR_INVALID, "%s rows must be 16-byte aligned", nm);
+      if (t == k_dst) {
+        ps = t->shape[2];
+        P = t->shape[0];
+      } else if (t->shape[2] != ps || t->shape[0] != P) {
+        return fail(DSV_ERR_INVALID, "k_dst and v_dst must have the same pages");
+      }
+    }
+    const int sh = log2_exact(ps);
+    if (sh < 0) return fail(DSV_ERR_UNSUPPORTED, "page size must be a power of two");
+    if (start + M > page_table->shape[0] * ps) return fail(DSV_ERR_INVALID, "tokens [start, start + M) exceed the page table");
+    a.pt = page_table->data;
+    a.pt_i64 = page_table->dtype == DSV_I64;
+    a.ps_shift = sh;
+    a.n_phys = P;
+    a.k_dst = static_cast<uint16_t*>(k_dst->data);
+    a.kd_sp = k_dst->stride[0];
+    a.kd_sh = k_dst->stride[1];
+    a.kd_st = k_dst->stride[2];
+    a.v_dst = static_cast<uint16_t*>(v_dst->data);
+    a.vd_sp = v_dst->stride[0];
+    a.vd_sh = v_dst->stride[1];
+    a.vd_st = v_dst->stride[2];
+  } else {
+    int64_t S = -1;
+    for (dsv_tensor* t : {k_dst, v_dst}) {
+      const char* nm = t == k_dst ? "k_dst" : "v_dst";
+      int64_t s3[3], st3[3];
+      if ((rc = last3(t, nm, s3, st3)) != DSV_OK) return rc;
+      if (s3[0] != Hk || s3[2] != D) return fail(DSV_ERR_INVALID, "%s must be [Hk, S, D]", nm);
+      if (S >= 0 && s3[1] != S) return fail(DSV_ERR_INVALID, "k_dst and v_dst must hold the same tokens");
+      S = s3[1];
+      if (t == k_dst) {
+        a.k_dst = static_cast<uint16_t*>(t->data);
+        a.kd_sh = st3[0];
+        a.kd_st = st3[1];
+      } else {
+        a.v_dst = static_cast<uint16_t*>(t->data);
+        a.vd_sh = st3[0];
+        a.vd_st = st3[1];
+      }
+    }
+    if (start + M > S) return fail(DSV_ERR_INVALID, "tokens [start, start + M) exceed the cache");
+  }
+  if (g_dry_run) return DSV_OK;
+  const hipError_t e = dsv::launch_append(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "kv append launch");
+  return DSV_OK;
+}
+
 int dsv_kv_commit(const dsv_tensor* kv, const dsv_tensor* page_table, int64_t start, const dsv_tensor* path,
                   const dsv_tensor* info, int64_t tree, void* stream) {
   int rc;

@@ -145,6 +145,24 @@ struct CommitArgs {
   const int64_t* info;       // info[3] = path length
 };
 
+// Arguments of the tree K/V append (+ RoPE).
+struct AppendArgs {
+  int f16;                   // 1: f16, 0: bf16
+  int M, Hk, H, D;
+  const uint16_t* k; int64_t k_sm, k_sh;   // [M, Hk, D] (token, head strides)
+  const uint16_t* v; int64_t v_sm, v_sh;
+  const uint16_t* q; int64_t q_sm, q_sh;   // optional [M, H, D]
+  uint16_t* q_out; int64_t qo_sm, qo_sh;
+  const uint16_t* cos; int64_t cs_m;       // optional [M, D] (nullptr: no RoPE)
+  const uint16_t* sin; int64_t sn_m;
+  uint16_t* k_dst; int64_t kd_sp, kd_sh, kd_st;  // page pool half [P, Hk, page, D] or dense [Hk, S, D]
+  uint16_t* v_dst; int64_t vd_sp, vd_sh, vd_st;
+  const void* pt;            // page table (nullptr: dense)
+  int pt_i64, ps_shift;
+  int64_t n_phys;
+  int64_t start;             // logical token of tree node 0
+};
+
 // ---------------------------------------------------------------------------
 // Launchers (defined in the .hip files, called by the C-ABI layer).
 // ---------------------------------------------------------------------------
@@ -155,6 +173,7 @@ int attn_blocks_per_cu();
 hipError_t launch_merge(const MergeArgs& a, hipStream_t s);
 hipError_t launch_accept(const AcceptArgs& a, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1);
 hipError_t launch_commit(const CommitArgs& a, hipStream_t s);
+hipError_t launch_append(const AppendArgs& a, hipStream_t s);
 // Vocabulary ranges of the acceptance statistics: sets a.chunk and a.nchunk
 // from the logits layout, T, M, V and the GPU's CU count.
 void accept_chunking(AcceptArgs& a, int cus);

@@ -70,6 +70,7 @@ SIGNATURES = {
          _SZ, _V],
     ),
     "dsv_kv_commit": (ctypes.c_int, [_P, _P, _I64, _P, _P, _I64, _V]),
+    "dsv_kv_append": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _I64, _P, _P, _V]),
 }
 
 _lib: Optional[ctypes.CDLL] = None

@@ -133,6 +133,35 @@ def test_kv_commit_validation(dsv_lib):
     assert rc == 0
 
 
+def test_kv_append_validation(dsv_lib):
+    none = _ext.DsvTensor()
+    k = _t((8, 2, 72))  # head_dim not a multiple of 16
+    dst = _t((2, 40, 72))
+    rc = dsv_lib.dsv_kv_append(ctypes.byref(k), ctypes.byref(k), ctypes.byref(none), ctypes.byref(none),
+                               ctypes.byref(dst), ctypes.byref(dst), ctypes.byref(none), 0, ctypes.byref(none),
+                               ctypes.byref(none), None)
+    assert rc == -2 and "multiple of 16" in _ext.last_error()
+    k = _t((8, 2, 64))
+    dst = _t((2, 40, 64))
+    rc = dsv_lib.dsv_kv_append(ctypes.byref(k), ctypes.byref(k), ctypes.byref(none), ctypes.byref(none),
+                               ctypes.byref(dst), ctypes.byref(dst), ctypes.byref(none), 35, ctypes.byref(none),
+                               ctypes.byref(none), None)
+    assert rc == -1 and "exceed the cache" in _ext.last_error()
+    cos = _t((8, 64))
+    rc = dsv_lib.dsv_kv_append(ctypes.byref(k), ctypes.byref(k), ctypes.byref(cos), ctypes.byref(none),
+                               ctypes.byref(dst), ctypes.byref(dst), ctypes.byref(none), 0, ctypes.byref(none),
+                               ctypes.byref(none), None)
+    assert rc == -1 and "together" in _ext.last_error()
+    dsv_lib.dsv_set_dry_run(1)
+    try:
+        rc = dsv_lib.dsv_kv_append(ctypes.byref(k), ctypes.byref(k), ctypes.byref(cos), ctypes.byref(cos),
+                                   ctypes.byref(dst), ctypes.byref(dst), ctypes.byref(none), 32, ctypes.byref(none),
+                                   ctypes.byref(none), None)
+    finally:
+        dsv_lib.dsv_set_dry_run(0)
+    assert rc == 0
+
+
 def test_python_api_refuses_cpu_tensors(dsv_lib):
     from diffspec_mi355x.runtime.tree_attention import prefix_attention_forward, tree_verify
     from diffspec_mi355x.draft.tree_verification import tree_accept

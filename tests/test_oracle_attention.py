@@ -177,3 +177,29 @@ def test_oracle_matches_reference_cpu_op_sequence():
     out = rc.hybrid_verify_cpu(q, kc, vc, N, rc.additive_tree_mask(keep))
     want, _ = oa.tree_verify(q[0].numpy(), kc[0].transpose(0, 1).numpy(), vc[0].transpose(0, 1).numpy(), N, parent)
     np.testing.assert_allclose(out[0].numpy(), want, atol=2e-5, rtol=1e-4)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_rope_16bit_matches_torch_elementwise_ops(dtype):
+    # The reference's op sequence on 16-bit tensors (torch CPU rounds each
+    # elementwise op to the dtype, as on the GPU).
+    g = torch.Generator().manual_seed(7)
+    M, H, D = 9, 3, 64
+    x = (torch.randn((H, M, D), generator=g) * 3).to(dtype)
+    pos = torch.arange(100, 100 + M, dtype=torch.float32)
+    inv = 1.0 / (5e5 ** (torch.arange(0, D, 2, dtype=torch.float32) / D))
+    emb = torch.cat([pos[:, None] * inv[None], pos[:, None] * inv[None]], -1)
+    cos, sin = emb.cos().to(dtype), emb.sin().to(dtype)
+
+    def rotate_half(t):
+        return torch.cat((-t[..., D // 2:], t[..., :D // 2]), dim=-1)
+
+    want = (x * cos) + (rotate_half(x) * sin)
+    got = oa.rope_16bit(x.float().numpy(), cos.float().numpy(), sin.float().numpy(), f16=dtype == torch.float16)
+    assert np.array_equal(got, want.float().numpy())
+    # cos = 1, sin = 0 is the identity; cos = 0, sin = 1 is rotate_half exactly.
+    one, zero = np.ones((M, D), np.float32), np.zeros((M, D), np.float32)
+    xf = x.float().numpy()
+    f16 = dtype == torch.float16
+    assert np.array_equal(oa.rope_16bit(xf, one, zero, f16=f16), xf)
+    assert np.array_equal(oa.rope_16bit(xf, zero, one, f16=f16), rotate_half(x).float().numpy())
