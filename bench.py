@@ -155,19 +155,24 @@ def bench_verify(args, lib, ev):
 
 def bench_config3(args, lib, ev):
     """128K paged prefix, 128-node tree (depth <= 12, out-degree <= 6), query
-    rows packed in bundle order (8 bundles).  MFMA-bound: 512 flop/B."""
+    rows packed in bundle order (8 bundles).  MFMA-bound: 512 flop/B.  A step
+    computes the bundle order on the GPU from the device parent array
+    (dsv_bundle_order), then runs the fused verify with it."""
     from diffspec_mi355x import workloads as wl
-    from diffspec_mi355x.core.bundle_scheduler import bundle_row_order
+    from diffspec_mi355x.core.bundle_scheduler import bundle_row_order, bundle_row_order_device
     from diffspec_mi355x.runtime.tree_attention import tree_verify
 
     N, M, H, Hk, D, layers = 131072, 128, 32, 8, 128, 3
     inp = wl.make_tree_verify_inputs(n_prefix=N, M=M, H=H, Hk=Hk, D=D, layers=layers, device="cuda", seed=2,
                                      tree_seed=2, max_depth=12, max_outdeg=6)
     par = torch.tensor(inp.parent, dtype=torch.int64, device="cuda")
-    perm = torch.tensor(bundle_row_order(inp.parent, num_bundles=8), dtype=torch.int32, device="cuda")
+    host_perm = torch.tensor(bundle_row_order(inp.parent, num_bundles=8), dtype=torch.int32, device="cuda")
+    if not torch.equal(bundle_row_order_device(par, num_bundles=8), host_perm):
+        raise RuntimeError("device bundle order differs from the host scheduler's")
     pools = [(inp.kv_pages[l, 0], inp.kv_pages[l, 1]) for l in range(layers)]
 
     def step(i, arm=None):
+        perm = bundle_row_order_device(par, num_bundles=8)
         if arm is not None:
             lib.dsv_set_timing_events(arm[0], arm[1])
         k, v = pools[i % layers]
@@ -190,6 +195,14 @@ def bench_config3(args, lib, ev):
     torch.cuda.synchronize()
     k1_us = statistics.mean(ev.elapsed_ms(evs[2 * i], evs[2 * i + 1]) for i in range(n)) * 1e3
     ev.destroy(evs)
+    # Bundle order: device time per launch vs the host scheduler + copy.
+    order_us = device_us(lambda: bundle_row_order_device(par, num_bundles=8))
+    t0 = time.perf_counter()
+    reps = 20
+    for _ in range(reps):
+        hp = torch.tensor(bundle_row_order(par.tolist(), num_bundles=8), dtype=torch.int32).to("cuda")
+    torch.cuda.synchronize()
+    host_us = (time.perf_counter() - t0) / reps * 1e6
     nb = algorithmic_bytes(N, M, H, Hk, D)
     flops = 4 * M * H * N * D + 4 * M * H * M * D
     return {"workload": "tree-verify attention, N=131072, M=128 (8 bundles, row-packed), paged bf16 KV, "
@@ -198,7 +211,11 @@ def bench_config3(args, lib, ev):
             "kernel1_mfma_frac": round(flops / (k1_us * 1e-6) / 2.5e15, 4),
             "kernel1_hbm_gbs": round(nb["kernel1"] / (k1_us * 1e-6) / 1e9, 1),
             "kernel1_hbm_frac": round(nb["kernel1"] / (k1_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-            "flops_dense": flops, "bytes_per_launch": nb["kernel1"]}
+            "flops_dense": flops, "bytes_per_launch": nb["kernel1"],
+            "bundle_order": {"device_us": round(order_us, 2),
+                             "host_scheduler_us": round(host_us, 1),
+                             "timing": "device: HIP graph replay; host: parent to host, Python "
+                                       "scheduler, permutation to the device"}}
 
 
 def device_us(fn, calls=10, reps=20):

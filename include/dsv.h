@@ -280,6 +280,37 @@ int dsv_kv_append(const dsv_tensor* k, const dsv_tensor* v, const dsv_tensor* co
                   const dsv_tensor* page_table, int64_t start, const dsv_tensor* q,
                   dsv_tensor* q_out, void* stream);
 
+/* ------------------------------------------------------------------------- */
+/* Bundle order (query packing permutation)                                   */
+/* ------------------------------------------------------------------------- */
+
+/*
+ * The node order that packs a tree's query rows bundle by bundle (the
+ * row_perm of dsv_tree_verify), computed on the GPU from the parent array.
+ * Replaces the host scheduling of verify_new (draft/tree_verification.py:139-159:
+ * descriptor with leaves in index order and depths) and
+ * BundleScheduler.schedule_bundles with its branching-ancestor and path
+ * helpers (core/bundle_scheduler.py:42-171): leaves bucketed by branching
+ * ancestor (buckets in the order of their lowest leaf), stably sorted by
+ * depth, cut into bundles of bundle_size leaves, at most max_bundles bundles;
+ * the order lists, bundle by bundle and leaf by leaf, the not yet listed
+ * nodes of each leaf's root path root first, then every node no emitted leaf
+ * covers, in index order.
+ *   parent       [M] or [B, M] int32|int64; a parent < 0, equal to the node or
+ *                >= M means none, node 0 is a root
+ *   bundle_size  leaves per bundle (>= 1) when num_bundles == 0
+ *   num_bundles  > 0: bundle_size = max(1, ceil(leaves / num_bundles))
+ *   max_bundles  bundles emitted; values below 1 emit one bundle, as the
+ *                scheduler checks the bound after adding a bundle
+ *   perm         [M] or [B, M] int32 (contiguous): perm[b, j] = node in row j
+ *   bundle_of    optional, shape of perm: bundle id of the leaf through which
+ *                each node was listed, -1 for uncovered nodes (ndim 0 to skip)
+ * 1 <= M <= 1024.  One launch, one workgroup per tree, no host round trip.
+ */
+int dsv_bundle_order(const dsv_tensor* parent, int64_t bundle_size,
+                     int64_t num_bundles, int64_t max_bundles, dsv_tensor* perm,
+                     dsv_tensor* bundle_of, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -924,6 +924,49 @@ int dsv_kv_commit(const dsv_tensor* kv, const dsv_tensor* page_table, int64_t st
   return DSV_OK;
 }
 
+int dsv_bundle_order(const dsv_tensor* parent, int64_t bundle_size, int64_t num_bundles, int64_t max_bundles,
+                     dsv_tensor* perm, dsv_tensor* bundle_of, void* stream) {
+  int rc;
+  if (parent == nullptr || (parent->ndim != 1 && parent->ndim != 2)) return fail(DSV_ERR_INVALID, "parent must be [M] or [B, M]");
+  if ((rc = check_nd(parent, "parent", parent->ndim)) != DSV_OK) return rc;
+  if (parent->dtype != DSV_I32 && parent->dtype != DSV_I64) return fail(DSV_ERR_INVALID, "parent must be int32 or int64");
+  const int nd = parent->ndim;
+  const int64_t B = nd == 2 ? parent->shape[0] : 1, M = parent->shape[nd - 1];
+  if (M < 1 || M > dsv::kBundleMaxNodes)
+    return fail(DSV_ERR_UNSUPPORTED, "trees of %lld nodes are not supported (1..%d)", (long long)M, dsv::kBundleMaxNodes);
+  if (B < 1 || B > 0x7fffffff) return fail(DSV_ERR_INVALID, "batch size out of range");
+  if (num_bundles < 0 || num_bundles > 0x7fffffff) return fail(DSV_ERR_INVALID, "num_bundles must be >= 0");
+  if (num_bundles == 0 && (bundle_size < 1 || bundle_size > 0x7fffffff))
+    return fail(DSV_ERR_INVALID, "bundle_size must be >= 1");
+  for (dsv_tensor* t : {perm, bundle_of}) {
+    const char* nm = t == perm ? "perm" : "bundle_of";
+    if (t == bundle_of && !present(t)) continue;
+    if (t == nullptr || t->ndim != nd) return fail(DSV_ERR_INVALID, "%s must have the shape of parent", nm);
+    if ((rc = check_nd(t, nm, nd)) != DSV_OK) return rc;
+    if (t->dtype != DSV_I32) return fail(DSV_ERR_INVALID, "%s must be int32", nm);
+    if (t->shape[nd - 1] != M || (nd == 2 && t->shape[0] != B)) return fail(DSV_ERR_INVALID, "%s must have the shape of parent", nm);
+    if (t->stride[nd - 1] != 1 || (nd == 2 && B > 1 && t->stride[0] != M)) return fail(DSV_ERR_INVALID, "%s must be contiguous", nm);
+  }
+  dsv::BundleArgs a{};
+  a.B = (int)B;
+  a.M = (int)M;
+  a.parent = parent->data;
+  a.p_i64 = parent->dtype == DSV_I64;
+  a.p_st = nd == 2 ? parent->stride[0] : 0;
+  a.p_sm = parent->stride[nd - 1];
+  a.bundle_size = num_bundles > 0 ? 1 : (int)bundle_size;
+  a.num_bundles = (int)num_bundles;
+  // The scheduler stops once it holds max_bundles bundles, checked after each
+  // one is added: at least one bundle is always emitted.
+  a.max_bundles = (int)std::min<int64_t>(std::max<int64_t>(max_bundles, 1), 0x7fffffff);
+  a.perm = static_cast<int32_t*>(perm->data);
+  a.bundle_of = present(bundle_of) ? static_cast<int32_t*>(bundle_of->data) : nullptr;
+  if (g_dry_run) return DSV_OK;
+  const hipError_t e = dsv::launch_bundle_order(a, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "bundle order launch");
+  return DSV_OK;
+}
+
 int dsv_tree_accept(int mode, const dsv_tensor* logits, const dsv_tensor* draft, const dsv_tensor* parent,
                     const dsv_tensor* pos, int64_t max_hops, float temperature, float posterior_threshold,
                     float posterior_alpha, dsv_tensor* out_path, dsv_tensor* out_tokens, dsv_tensor* out_info,

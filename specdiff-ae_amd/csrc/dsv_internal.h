@@ -163,6 +163,20 @@ struct AppendArgs {
   int64_t start;             // logical token of tree node 0
 };
 
+// Arguments of the bundle order (query packing permutation) of B trees.
+constexpr int kBundleMaxNodes = 1024;
+constexpr int kBundleThreads = 256;        // lanes per workgroup at most (<= 4 nodes each)
+struct BundleArgs {
+  int B, M;
+  const void* parent; int p_i64;           // [B, M] int32|int64
+  int64_t p_st, p_sm;
+  int bundle_size;                         // leaves per bundle (num_bundles == 0)
+  int num_bundles;                         // > 0: bundle_size = ceil(leaves / num_bundles)
+  int max_bundles;                         // bundles emitted (>= 1)
+  int32_t* perm;                           // [B, M] node order
+  int32_t* bundle_of;                      // optional [B, M] bundle of each node (-1: none)
+};
+
 // ---------------------------------------------------------------------------
 // Launchers (defined in the .hip files, called by the C-ABI layer).
 // ---------------------------------------------------------------------------
@@ -174,6 +188,7 @@ hipError_t launch_merge(const MergeArgs& a, hipStream_t s);
 hipError_t launch_accept(const AcceptArgs& a, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1);
 hipError_t launch_commit(const CommitArgs& a, hipStream_t s);
 hipError_t launch_append(const AppendArgs& a, hipStream_t s);
+hipError_t launch_bundle_order(const BundleArgs& a, hipStream_t s);
 // Vocabulary ranges of the acceptance statistics: sets a.chunk and a.nchunk
 // from the logits layout, T, M, V and the GPU's CU count.
 void accept_chunking(AcceptArgs& a, int cus);

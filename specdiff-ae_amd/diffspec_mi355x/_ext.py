@@ -71,6 +71,7 @@ SIGNATURES = {
     ),
     "dsv_kv_commit": (ctypes.c_int, [_P, _P, _I64, _P, _P, _I64, _V]),
     "dsv_kv_append": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _I64, _P, _P, _V]),
+    "dsv_bundle_order": (ctypes.c_int, [_P, _I64, _I64, _I64, _P, _P, _V]),
 }
 
 _lib: Optional[ctypes.CDLL] = None

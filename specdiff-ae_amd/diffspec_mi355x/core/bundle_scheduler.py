@@ -19,7 +19,9 @@ once per leaf, so scheduling is O(N) instead of O(leaves * N).
 ``bundle_row_order`` turns a schedule into the node permutation used by the
 tree-attention kernel to pack query rows: nodes of one bundle (the union of
 its leaves' root paths) become adjacent rows, so rows sharing ancestors share
-K/V tiles of the tree block.
+K/V tiles of the tree block.  ``bundle_row_order_device`` computes the same
+permutation on the GPU from a device parent tensor (one launch, no host round
+trip between the draft tree and the verify launch).
 """
 
 from __future__ import annotations
@@ -262,3 +264,29 @@ def bundle_row_order(parent: Sequence[int], bundle_size: int = 3, max_bundles: i
                 order.append(node)
     order.extend(i for i in range(len(parent)) if i not in placed)
     return order
+
+
+def bundle_row_order_device(parent: torch.Tensor, bundle_size: int = 3, max_bundles: int = 1 << 30,
+                            num_bundles: Optional[int] = None, return_bundles: bool = False):
+    """``bundle_row_order`` computed on the GPU (libdsv ``dsv_bundle_order``).
+
+    ``parent``: device int32/int64 ``[M]`` or ``[B, M]`` per-node parents
+    (< 0, equal to the node or >= M: none; node 0 is a root), M <= 1024.
+    Returns the int32 permutation (same shape; row j packs node perm[..., j]),
+    and with ``return_bundles`` also the int32 bundle id of the leaf through
+    which each node was placed (-1 for nodes no emitted bundle covers).
+    For a tree, the result equals ``bundle_row_order(parent.tolist(), ...)``
+    (schedule of the reference's core/bundle_scheduler.py:42-171).
+    """
+    from .. import _ext
+
+    _ext.require_gpu(parent)
+    if parent.dim() not in (1, 2):
+        raise ValueError("parent must be [M] or [B, M]")
+    perm = torch.empty(parent.shape, dtype=torch.int32, device=parent.device)
+    bof = torch.empty_like(perm) if return_bundles else None
+    lib = _ext.load()
+    rc = lib.dsv_bundle_order(_ext.desc(parent), int(bundle_size), int(num_bundles or 0), int(max_bundles),
+                              _ext.desc(perm), _ext.desc(bof), _ext.stream_of(parent.device))
+    _ext.check(rc, "bundle_order")
+    return (perm, bof) if return_bundles else perm

@@ -162,6 +162,31 @@ def test_kv_append_validation(dsv_lib):
     assert rc == 0
 
 
+def test_bundle_order_validation(dsv_lib):
+    none = _ext.DsvTensor()
+    par = _t((2000,), _ext.DSV_I64)
+    perm = _t((2000,), _ext.DSV_I32)
+    rc = dsv_lib.dsv_bundle_order(ctypes.byref(par), 3, 0, 100, ctypes.byref(perm), ctypes.byref(none), None)
+    assert rc == -2 and "1..1024" in _ext.last_error()
+    par = _t((2, 64), _ext.DSV_I32)
+    perm = _t((2, 64), _ext.DSV_I32)
+    rc = dsv_lib.dsv_bundle_order(ctypes.byref(par), 0, 0, 100, ctypes.byref(perm), ctypes.byref(none), None)
+    assert rc == -1 and "bundle_size" in _ext.last_error()
+    bad = _t((2, 64), _ext.DSV_I64)
+    rc = dsv_lib.dsv_bundle_order(ctypes.byref(par), 3, 0, 100, ctypes.byref(bad), ctypes.byref(none), None)
+    assert rc == -1 and "int32" in _ext.last_error()
+    bad = _t((64,), _ext.DSV_I32)
+    rc = dsv_lib.dsv_bundle_order(ctypes.byref(par), 3, 0, 100, ctypes.byref(perm), ctypes.byref(bad), None)
+    assert rc == -1 and "shape of parent" in _ext.last_error()
+    dsv_lib.dsv_set_dry_run(1)
+    try:
+        # num_bundles > 0 overrides bundle_size; max_bundles < 1 means one bundle
+        rc = dsv_lib.dsv_bundle_order(ctypes.byref(par), 0, 8, 0, ctypes.byref(perm), ctypes.byref(perm), None)
+    finally:
+        dsv_lib.dsv_set_dry_run(0)
+    assert rc == 0
+
+
 def test_python_api_refuses_cpu_tensors(dsv_lib):
     from diffspec_mi355x.runtime.tree_attention import prefix_attention_forward, tree_verify
     from diffspec_mi355x.draft.tree_verification import tree_accept
