@@ -9,6 +9,8 @@ Modules
   attention     numpy float64 closed forms of the attention path (A1-A8)
   accept        restatement of the greedy walk (draft/tree_verification.py:100-182),
                 the typical (posterior) walk and an independent brute force
+  bundles       restatement of the bundle scheduler (core/bundle_scheduler.py:42-171)
+                and the query packing order built from it
   ref_cpu_path  the reference's own torch CPU op sequence (repeat_kv -> prefix
                 matmul/softmax/logsumexp -> naive tree -> sigmoid merge -> walk),
                 timed as the CPU baseline
@@ -20,6 +22,8 @@ Pinning (what each function is checked against, besides the GPU):
   ancestor_mask         brute-force walk and the bitmask recurrence
   greedy_walk           brute force over root paths, hand-made trees (ties,
                         full accept, root only) — tests/test_oracle_accept.py
+  bundles.packing_order the reference's scheduler vectors, hand-worked orders,
+                        invariants on generated trees — tests/test_oracle_bundles.py
   typical_walk          closed forms of the entropy (uniform, one-hot) and the
                         greedy/typical relation on planted cases.  The reference
                         has no typical acceptance: parity with the reference is
