@@ -251,7 +251,7 @@ def bench_config5(args, lib, ev):
     (kernel 4).  Projections, norms and the MLP are torch (hipBLASLt) ops:
     measurement scaffolding around the hot path, not part of it."""
     from diffspec_mi355x import workloads as wl
-    from diffspec_mi355x.draft.tree_verification import tree_accept
+    from diffspec_mi355x.draft.tree_verification import lmhead_tree_accept, tree_accept
     from diffspec_mi355x.runtime.cache_state import append_tree_kv
     from diffspec_mi355x.runtime.tree_attention import tree_verify
 
@@ -265,7 +265,7 @@ def bench_config5(args, lib, ev):
         return (torch.randn(shape, generator=g, device=dev) * 0.02).to(torch.bfloat16)
 
     layers = [dict(qkv=w(hid, (H + 2 * Hk) * D), o=w(H * D, hid), gu=w(hid, 2 * F), d=w(F, hid)) for _ in range(L)]
-    lm_head = w(hid, V)
+    lm_head = w(V, hid)  # nn.Linear(hid, V).weight layout
     x0 = w(M, hid) * 50
     par = torch.tensor(inp.parent, dtype=torch.int64, device=dev)
     pref = torch.tensor([[p - 1 for p in inp.parent[1:]]], dtype=torch.int64, device=dev)
@@ -309,8 +309,8 @@ def bench_config5(args, lib, ev):
             x = x + o.view(M, H * D) @ W["o"]
             gu = rms(x) @ W["gu"]
             x = x + (torch.nn.functional.silu(gu[:, :F].float()) * gu[:, F:].float()).to(torch.bfloat16) @ W["d"]
-        logits = rms(x) @ lm_head
-        return tree_accept(logits.unsqueeze(0), draft, pref, pos, 10)
+        # lm_head fused with the greedy acceptance (kernel 5 + the walk)
+        return lmhead_tree_accept(rms(x).unsqueeze(0), lm_head, draft, pref, pos, 10)
 
     for _ in range(3):
         step()
@@ -345,6 +345,7 @@ def bench_config5(args, lib, ev):
 
     app = {"us": round(device_us(ours), 2), "reference_ops_us": round(device_us(theirs), 2),
            "timing": "device time per call, HIP graph of 10 calls replayed"}
+    lmh = bench_lmhead(lm_head, x0, draft, pref, pos, rms)
     wbytes = sum(t.numel() * 2 for W in layers for t in W.values()) + lm_head.numel() * 2
     kvbytes = L * algorithmic_bytes(N, M, H, Hk, D)["prefix_kv"]
     return {"workload": "Llama-3.1-8B-shaped verify step: 32 layers, 64-node tree, 65536-token paged prefix per "
@@ -353,7 +354,32 @@ def bench_config5(args, lib, ev):
             "attention_share": round(attn_us / us_step, 3), "weight_bytes": wbytes, "kv_bytes": kvbytes,
             "hbm_gbs": round((wbytes + kvbytes) / (us_step * 1e-6) / 1e9, 1),
             "accept_length": int(r["info"][0, 1]), "kv_commit": commit,
-            "kv_append_one_layer": dict(app, bytes=(M * (H + 2 * Hk) * D * 2) * 2)}
+            "kv_append_one_layer": dict(app, bytes=(M * (H + 2 * Hk) * D * 2) * 2), "lmhead_accept": lmh}
+
+
+def bench_lmhead(lm_head, x0, draft, pref, pos, rms):
+    """lm_head + greedy acceptance of a 64-node tree (Dm 4096, V 128256):
+    the fused kernel against torch's lm_head (hipBLASLt, x @ W^T) followed by
+    kernel 4 on the materialised bf16 logits."""
+    from diffspec_mi355x.draft.tree_verification import lmhead_tree_accept, tree_accept
+
+    xn = rms(x0)
+    V, hid = lm_head.shape
+    M = xn.shape[0]
+    fused = device_us(lambda: lmhead_tree_accept(xn.unsqueeze(0), lm_head, draft, pref, pos, 10), calls=5, reps=10)
+    mm = device_us(lambda: xn @ lm_head.T, calls=5, reps=10)
+    unfused = device_us(lambda: tree_accept((xn @ lm_head.T).unsqueeze(0), draft, pref, pos, 10), calls=5, reps=10)
+    nb = V * hid * 2 + M * hid * 2
+    rf = lmhead_tree_accept(xn.unsqueeze(0), lm_head, draft, pref, pos, 10, return_next=True)
+    ru = tree_accept((xn @ lm_head.T).unsqueeze(0), draft, pref, pos, 10, return_next=True)
+    same_next = float((rf["next"] == ru["next"]).float().mean())
+    return {"workload": "lm_head [128256 x 4096] bf16 over 64 tree nodes + greedy walk",
+            "fused_us": round(fused, 2), "torch_lm_head_us": round(mm, 2),
+            "torch_lm_head_plus_kernel4_us": round(unfused, 2), "bytes": nb,
+            "fused_hbm_gbs": round(nb / (fused * 1e-6) / 1e9, 1),
+            "fused_hbm_frac": round(nb / (fused * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "next_token_agreement_with_torch_logits": same_next,
+            "timing": "device time per call, HIP graph of 5 calls replayed"}
 
 
 def bench_commit(inp, N, M, L, Hk, D, n):

@@ -252,6 +252,37 @@ int dsv_kv_commit(const dsv_tensor* kv, const dsv_tensor* page_table, int64_t st
                   void* stream);
 
 /* ------------------------------------------------------------------------- */
+/* lm_head fused with the acceptance (kernel 5 + kernel 4's walk)             */
+/* ------------------------------------------------------------------------- */
+
+/* Workspace for dsv_lmhead_accept with T trees of M nodes over vocab V. */
+size_t dsv_lmhead_accept_workspace_bytes(int64_t T, int64_t M, int64_t V);
+
+/*
+ * dsv_tree_accept over logits = hidden . weight^T computed in the same
+ * launch sequence, without writing the logits: replaces the target's
+ * self.base_model.lm_head(hidden_states) (draft/diffspec_model.py:229-231)
+ * followed by the walk of verify_new (draft/tree_verification.py:100-182).
+ * Every logit is rounded to bf16 before the argmax and the softmax
+ * statistics, as the reference's bf16 logits are.
+ *   hidden      [T, M, Dm] bf16 (rows of all trees at one stride); Dm a
+ *               multiple of 64
+ *   weight      [V, Dm] bf16 (nn.Linear.weight), rows 16-byte aligned
+ *   draft, parent, pos, max_hops, temperature, thresholds, out_*: as
+ *               dsv_tree_accept
+ *   logits_out  optional bf16 [T, M, V]: also write the logits (ndim 0 to skip)
+ * The weight is streamed once per 64 hidden rows (T * M <= 64: once).
+ */
+int dsv_lmhead_accept(int mode, const dsv_tensor* hidden, const dsv_tensor* weight,
+                      const dsv_tensor* draft, const dsv_tensor* parent,
+                      const dsv_tensor* pos, int64_t max_hops, float temperature,
+                      float posterior_threshold, float posterior_alpha,
+                      dsv_tensor* out_path, dsv_tensor* out_tokens,
+                      dsv_tensor* out_info, dsv_tensor* out_next,
+                      dsv_tensor* logits_out, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------- */
 /* Tree K/V append with RoPE                                                  */
 /* ------------------------------------------------------------------------- */
 

@@ -26,6 +26,7 @@
 #include <algorithm>
 
 #include "dsv_internal.h"
+#include "dsv_stats.h"
 
 namespace dsv {
 
@@ -35,33 +36,6 @@ constexpr float kNegInf = -__builtin_huge_valf();
 constexpr float kLog2e = 1.4426950408889634074f;
 constexpr float kLn2 = 0.69314718055994530942f;
 constexpr int kRowThreads = 256;
-
-struct ArgMax {
-  float v;
-  int i;
-};
-
-// a ranks before b: larger value, NaN above all numbers, ties -> lower index.
-__device__ __forceinline__ bool am_better(float av, int ai, float bv, int bi) {
-  const bool an = av != av, bn = bv != bv;
-  if (an || bn) return an && (!bn || ai < bi);
-  if (av != bv) return av > bv;
-  return ai < bi;
-}
-
-struct Soft {
-  float m;  // max of y*log2e
-  float l;  // sum 2^(z - m)
-  float s;  // sum y * 2^(z - m)
-};
-
-__device__ __forceinline__ Soft soft_merge(Soft a, Soft b) {
-  if (a.m == kNegInf) return b;
-  if (b.m == kNegInf) return a;
-  const float m = fmaxf(a.m, b.m);
-  const float fa = __builtin_amdgcn_exp2f(a.m - m), fb = __builtin_amdgcn_exp2f(b.m - m);
-  return Soft{m, a.l * fa + b.l * fb, a.s * fa + b.s * fb};
-}
 
 template <typename LT>
 __device__ __forceinline__ float to_f(LT x);
@@ -574,7 +548,9 @@ __global__ void __launch_bounds__(1024) accept_walk_kernel(const AcceptArgs a) {
   if (i > 0 && i < M && a.mode == 1) {
     const int p = par[i];  // written by this thread
     tok_ok = tok >= 0 && tok < a.V;
-    if (tok_ok) {
+    if (tok_ok && a.xtok != nullptr) {
+      xtok = a.xtok[(int64_t)t * M + i];  // computed with the statistics (fused lm_head)
+    } else if (tok_ok) {
       const int64_t off = (int64_t)t * a.l_st + (int64_t)p * a.l_sm + tok;
       if (a.l_dtype == 0)
         xtok = __uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(a.logits)[off] << 16);
@@ -707,7 +683,85 @@ hipError_t launch_rowstat(const AcceptArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Reduces the nin partial statistics of every row (row-major [rows, nin])
+// to one per row in a.rstat / a.rstat2 (a.nchunk == 1): argmax with the
+// lowest index on ties, softmax statistics by rescaled merges.
+template <bool TYPICAL>
+__global__ void __launch_bounds__(kRowThreads) accept_combine_kernel(const AcceptArgs a, const float4* part,
+                                                                     const float* part2, int nin) {
+  const int64_t row = blockIdx.x;
+  ArgMax best{kNegInf, 0x7fffffff};
+  bool have = false;
+  Soft sm{kNegInf, 0.f, 0.f};
+  for (int c = threadIdx.x; c < nin; c += kRowThreads) {
+    const float4 st = part[row * nin + c];
+    const int ci = __float_as_int(st.y);
+    if (ci >= 0 && (!have || am_better(st.x, ci, best.v, best.i))) {
+      best.v = st.x;
+      best.i = ci;
+      have = true;
+    }
+    if constexpr (TYPICAL) sm = soft_merge(sm, Soft{st.z, st.w, part2[row * nin + c]});
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(best.v, o);
+    const int oi = __shfl_xor(best.i, o);
+    const int oh = __shfl_xor((int)have, o);
+    if (oh && (!have || am_better(ov, oi, best.v, best.i))) {
+      best.v = ov;
+      best.i = oi;
+      have = true;
+    }
+    if constexpr (TYPICAL) {
+      Soft other{__shfl_xor(sm.m, o), __shfl_xor(sm.l, o), __shfl_xor(sm.s, o)};
+      sm = soft_merge(sm, other);
+    }
+  }
+  __shared__ float sv[kRowThreads / 64], sm_m[kRowThreads / 64], sm_l[kRowThreads / 64], sm_s[kRowThreads / 64];
+  __shared__ int si[kRowThreads / 64], sh[kRowThreads / 64];
+  const int wid = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    sv[wid] = best.v;
+    si[wid] = best.i;
+    sh[wid] = have;
+    sm_m[wid] = sm.m;
+    sm_l[wid] = sm.l;
+    sm_s[wid] = sm.s;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int x = 1; x < kRowThreads / 64; ++x) {
+      if (sh[x] && (!have || am_better(sv[x], si[x], best.v, best.i))) {
+        best.v = sv[x];
+        best.i = si[x];
+        have = true;
+      }
+      if constexpr (TYPICAL) sm = soft_merge(sm, Soft{sm_m[x], sm_l[x], sm_s[x]});
+    }
+    a.rstat[row] = make_float4(best.v, __int_as_float(have ? best.i : -1), sm.m, sm.l);
+    if constexpr (TYPICAL) a.rstat2[row] = sm.s;
+  }
+}
+
 }  // namespace
+
+size_t accept_walk_lds_bytes(int M);
+
+hipError_t launch_accept_from_parts(const AcceptArgs& a, const float4* part, const float* part2, int nin,
+                                    hipStream_t s) {
+  if (a.T <= 0 || a.M <= 0) return hipSuccess;
+  const dim3 grid((unsigned)((int64_t)a.T * a.M));
+  if (a.mode == 1)
+    hipLaunchKernelGGL(accept_combine_kernel<true>, grid, dim3(kRowThreads), 0, s, a, part, part2, nin);
+  else
+    hipLaunchKernelGGL(accept_combine_kernel<false>, grid, dim3(kRowThreads), 0, s, a, part, part2, nin);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int threads = ((a.M + 63) / 64) * 64;
+  hipLaunchKernelGGL(accept_walk_kernel, dim3((unsigned)a.T), dim3(threads), accept_walk_lds_bytes(a.M), s, a);
+  return hipGetLastError();
+}
 
 size_t accept_walk_lds_bytes(int M) {
   // par, nxt, ok, mz, lz, hz, path: 7*M words, plus reduction scratch.

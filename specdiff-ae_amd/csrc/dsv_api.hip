@@ -967,23 +967,27 @@ int dsv_bundle_order(const dsv_tensor* parent, int64_t bundle_size, int64_t num_
   return DSV_OK;
 }
 
-int dsv_tree_accept(int mode, const dsv_tensor* logits, const dsv_tensor* draft, const dsv_tensor* parent,
-                    const dsv_tensor* pos, int64_t max_hops, float temperature, float posterior_threshold,
-                    float posterior_alpha, dsv_tensor* out_path, dsv_tensor* out_tokens, dsv_tensor* out_info,
-                    dsv_tensor* out_next, void* workspace, size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+// Validation and arguments shared by both acceptance entry points: tree
+// shape (T, M), vocabulary V, the tree tensors and the outputs.
+static int accept_common(int mode, int64_t T, int64_t M, int64_t V, const dsv_tensor* draft,
+                         const dsv_tensor* parent, const dsv_tensor* pos, int64_t max_hops, float temperature,
+                         float posterior_threshold, float posterior_alpha, dsv_tensor* out_path,
+                         dsv_tensor* out_tokens, dsv_tensor* out_info, dsv_tensor* out_next, dsv::AcceptArgs& a) {
   int rc;
-  if (mode != DSV_ACCEPT_GREEDY && mode != DSV_ACCEPT_TYPICAL) return fail(DSV_ERR_INVALID, "unknown acceptance mode %d", mode);
-  if ((rc = check_nd(logits, "logits", 3)) != DSV_OK) return rc;
-  if (logits->dtype != DSV_BF16 && logits->dtype != DSV_F16 && logits->dtype != DSV_F32)
-    return fail(DSV_ERR_INVALID, "logits must be bf16, f16 or f32");
-  if (logits->stride[2] != 1) return fail(DSV_ERR_INVALID, "logits vocab stride must be 1");
-  const int64_t T = logits->shape[0], M = logits->shape[1], V = logits->shape[2];
   if (M < 1 || M > 1024) return fail(DSV_ERR_UNSUPPORTED, "trees of %lld nodes are not supported (1..1024)", (long long)M);
   if (V < 1 || V > 0x7fffffff) return fail(DSV_ERR_INVALID, "vocab size out of range");
   if ((rc = check_nd(draft, "draft", 2)) != DSV_OK) return rc;
   if (draft->dtype != DSV_I64 || draft->shape[0] != T || draft->shape[1] != M)
     return fail(DSV_ERR_INVALID, "draft must be int64 [T, M]");
-  if ((rc = check_nd(parent, "parent", 2)) != DSV_OK) return rc;
+  // A root-only tree (M == 1) has an empty parent tensor, possibly without
+  // storage; nothing reads it then.
+  if (M > 1) {
+    if ((rc = check_nd(parent, "parent", 2)) != DSV_OK) return rc;
+  } else if (parent == nullptr || parent->ndim != 2) {
+    return fail(DSV_ERR_INVALID, "parent must be int64 [T, M-1]");
+  }
   if (parent->dtype != DSV_I64 || parent->shape[0] != T || parent->shape[1] != M - 1)
     return fail(DSV_ERR_INVALID, "parent must be int64 [T, M-1]");
   if (pos == nullptr || (pos->ndim != 1 && pos->ndim != 2)) return fail(DSV_ERR_INVALID, "pos must be [M] or [T, M]");
@@ -1003,17 +1007,8 @@ int dsv_tree_accept(int mode, const dsv_tensor* logits, const dsv_tensor* draft,
   if ((rc = chk_out(out_tokens, "out_tokens", M)) != DSV_OK) return rc;
   if ((rc = chk_out(out_info, "out_info", 4)) != DSV_OK) return rc;
   if (present(out_next) && (rc = chk_out(out_next, "out_next", M)) != DSV_OK) return rc;
-  const size_t need = dsv_accept_workspace_bytes(T, M, V);
-  if (workspace == nullptr || workspace_bytes < need)
-    return fail(DSV_ERR_WORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace_bytes);
-  if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0) return fail(DSV_ERR_WORKSPACE, "workspace must be 256-byte aligned");
 
-  AcceptArgs a{};
   a.mode = mode;
-  a.logits = logits->data;
-  a.l_dtype = logits->dtype;
-  a.l_st = logits->stride[0];
-  a.l_sm = logits->stride[1];
   a.T = (int)T;
   a.M = (int)M;
   a.V = V;
@@ -1030,10 +1025,6 @@ int dsv_tree_accept(int mode, const dsv_tensor* logits, const dsv_tensor* draft,
   a.inv_temp = mode == DSV_ACCEPT_TYPICAL ? 1.f / temperature : 1.f;
   a.eps = posterior_threshold;
   a.alpha = posterior_alpha;
-  dsv::accept_chunking(a, device_cus());
-  const size_t rows = (size_t)T * M * a.nchunk;
-  a.rstat = static_cast<float4*>(workspace);
-  a.rstat2 = reinterpret_cast<float*>(static_cast<char*>(workspace) + align_up(rows * 16, 256));
   a.out_path = static_cast<int64_t*>(out_path->data);
   a.op_st = out_path->stride[0];
   a.out_tok = static_cast<int64_t*>(out_tokens->data);
@@ -1044,10 +1035,134 @@ int dsv_tree_accept(int mode, const dsv_tensor* logits, const dsv_tensor* draft,
     a.out_next = static_cast<int64_t*>(out_next->data);
     a.on_st = out_next->stride[0];
   }
+  return DSV_OK;
+}
+
+extern "C" {
+
+int dsv_tree_accept(int mode, const dsv_tensor* logits, const dsv_tensor* draft, const dsv_tensor* parent,
+                    const dsv_tensor* pos, int64_t max_hops, float temperature, float posterior_threshold,
+                    float posterior_alpha, dsv_tensor* out_path, dsv_tensor* out_tokens, dsv_tensor* out_info,
+                    dsv_tensor* out_next, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc;
+  if (mode != DSV_ACCEPT_GREEDY && mode != DSV_ACCEPT_TYPICAL) return fail(DSV_ERR_INVALID, "unknown acceptance mode %d", mode);
+  if ((rc = check_nd(logits, "logits", 3)) != DSV_OK) return rc;
+  if (logits->dtype != DSV_BF16 && logits->dtype != DSV_F16 && logits->dtype != DSV_F32)
+    return fail(DSV_ERR_INVALID, "logits must be bf16, f16 or f32");
+  if (logits->stride[2] != 1) return fail(DSV_ERR_INVALID, "logits vocab stride must be 1");
+  const int64_t T = logits->shape[0], M = logits->shape[1], V = logits->shape[2];
+  AcceptArgs a{};
+  if ((rc = accept_common(mode, T, M, V, draft, parent, pos, max_hops, temperature, posterior_threshold,
+                          posterior_alpha, out_path, out_tokens, out_info, out_next, a)) != DSV_OK)
+    return rc;
+  const size_t need = dsv_accept_workspace_bytes(T, M, V);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(DSV_ERR_WORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace_bytes);
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0) return fail(DSV_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+
+  a.logits = logits->data;
+  a.l_dtype = logits->dtype;
+  a.l_st = logits->stride[0];
+  a.l_sm = logits->stride[1];
+  dsv::accept_chunking(a, device_cus());
+  const size_t rows = (size_t)T * M * a.nchunk;
+  a.rstat = static_cast<float4*>(workspace);
+  a.rstat2 = reinterpret_cast<float*>(static_cast<char*>(workspace) + align_up(rows * 16, 256));
   hipEvent_t ev0, ev1;
   take_events(ev0, ev1);
   hipError_t e = dsv::launch_accept(a, static_cast<hipStream_t>(stream), ev0, ev1);
   if (e != hipSuccess) return hip_fail(e, "acceptance kernel launch");
+  return DSV_OK;
+}
+
+size_t dsv_lmhead_accept_workspace_bytes(int64_t T, int64_t M, int64_t V) {
+  if (T <= 0 || M <= 0 || V <= 0) return 0;
+  const size_t R = (size_t)T * M, parts = R * (size_t)dsv::lmhead_blocks(V);
+  return align_up(parts * 16, 256) + align_up(parts * 4, 256) + align_up(R * 16, 256) + 2 * align_up(R * 4, 256);
+}
+
+int dsv_lmhead_accept(int mode, const dsv_tensor* hidden, const dsv_tensor* weight, const dsv_tensor* draft,
+                      const dsv_tensor* parent, const dsv_tensor* pos, int64_t max_hops, float temperature,
+                      float posterior_threshold, float posterior_alpha, dsv_tensor* out_path, dsv_tensor* out_tokens,
+                      dsv_tensor* out_info, dsv_tensor* out_next, dsv_tensor* logits_out, void* workspace,
+                      size_t workspace_bytes, void* stream) {
+  int rc;
+  if (mode != DSV_ACCEPT_GREEDY && mode != DSV_ACCEPT_TYPICAL) return fail(DSV_ERR_INVALID, "unknown acceptance mode %d", mode);
+  if ((rc = check_nd(hidden, "hidden", 3)) != DSV_OK) return rc;
+  if ((rc = check_nd(weight, "weight", 2)) != DSV_OK) return rc;
+  if (hidden->dtype != DSV_BF16 || weight->dtype != DSV_BF16) return fail(DSV_ERR_UNSUPPORTED, "hidden and weight must be bf16");
+  const int64_t T = hidden->shape[0], M = hidden->shape[1], Dm = hidden->shape[2], V = weight->shape[0];
+  if (weight->shape[1] != Dm) return fail(DSV_ERR_INVALID, "weight must be [V, %lld]", (long long)Dm);
+  if (Dm < dsv::kLmK || Dm % dsv::kLmK != 0 || Dm > (1 << 20))
+    return fail(DSV_ERR_UNSUPPORTED, "hidden size %lld must be a positive multiple of %d", (long long)Dm, dsv::kLmK);
+  if (hidden->stride[2] != 1 || weight->stride[1] != 1) return fail(DSV_ERR_INVALID, "hidden and weight rows must be contiguous");
+  if (hidden->stride[0] != M * hidden->stride[1] && T > 1)
+    return fail(DSV_ERR_INVALID, "hidden rows of all trees must share one stride ([T*M, Dm] view)");
+  if ((reinterpret_cast<uintptr_t>(hidden->data) & 15) != 0 || (reinterpret_cast<uintptr_t>(weight->data) & 15) != 0 ||
+      hidden->stride[1] % 8 != 0 || weight->stride[0] % 8 != 0)
+    return fail(DSV_ERR_INVALID, "hidden and weight rows must be 16-byte aligned");
+  AcceptArgs a{};
+  if ((rc = accept_common(mode, T, M, V, draft, parent, pos, max_hops, temperature, posterior_threshold,
+                          posterior_alpha, out_path, out_tokens, out_info, out_next, a)) != DSV_OK)
+    return rc;
+  if (present(logits_out)) {
+    if ((rc = check_nd(logits_out, "logits_out", 3)) != DSV_OK) return rc;
+    if (logits_out->dtype != DSV_BF16 || logits_out->shape[0] != T || logits_out->shape[1] != M ||
+        logits_out->shape[2] != V || logits_out->stride[2] != 1 || (T > 1 && logits_out->stride[0] != M * logits_out->stride[1]))
+      return fail(DSV_ERR_INVALID, "logits_out must be bf16 [T, M, V] with rows of one stride");
+  }
+  const size_t need = dsv_lmhead_accept_workspace_bytes(T, M, V);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(DSV_ERR_WORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace_bytes);
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0) return fail(DSV_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+
+  dsv::LmArgs lm{};
+  lm.mode = mode;
+  lm.h = static_cast<const uint16_t*>(hidden->data);
+  lm.ldh = hidden->stride[1];
+  lm.w = static_cast<const uint16_t*>(weight->data);
+  lm.ldw = weight->stride[0];
+  lm.R = (int)(T * M);
+  lm.Dm = (int)Dm;
+  lm.V = V;
+  lm.T = (int)T;
+  lm.M = (int)M;
+  lm.draft = a.draft;
+  lm.d_st = a.d_st;
+  lm.d_sm = a.d_sm;
+  lm.parent = a.parent;
+  lm.p_st = a.p_st;
+  lm.p_sm = a.p_sm;
+  lm.inv_temp = a.inv_temp;
+  lm.nblk = dsv::lmhead_blocks(V);
+  const size_t R = (size_t)T * M, parts = R * (size_t)lm.nblk;
+  char* ws = static_cast<char*>(workspace);
+  lm.rstat = reinterpret_cast<float4*>(ws);
+  ws += align_up(parts * 16, 256);
+  lm.rstat2 = reinterpret_cast<float*>(ws);
+  ws += align_up(parts * 4, 256);
+  a.rstat = reinterpret_cast<float4*>(ws);
+  ws += align_up(R * 16, 256);
+  a.rstat2 = reinterpret_cast<float*>(ws);
+  ws += align_up(R * 4, 256);
+  lm.xtok = reinterpret_cast<float*>(ws);
+  a.xtok = lm.xtok;
+  a.nchunk = 1;
+  a.chunk = V;
+  if (present(logits_out)) {
+    lm.lout = static_cast<uint16_t*>(logits_out->data);
+    lm.lo_sr = logits_out->stride[1];
+  }
+  if (g_dry_run) return DSV_OK;
+  hipEvent_t ev0, ev1;
+  take_events(ev0, ev1);
+  hipError_t e;
+  if (ev0 != nullptr && (e = hipEventRecord(ev0, static_cast<hipStream_t>(stream))) != hipSuccess)
+    return hip_fail(e, "timing event");
+  e = dsv::launch_lmhead_accept(a, lm, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "lm_head acceptance launch");
+  if (ev1 != nullptr && (e = hipEventRecord(ev1, static_cast<hipStream_t>(stream))) != hipSuccess)
+    return hip_fail(e, "timing event");
   return DSV_OK;
 }
 

@@ -122,6 +122,7 @@ struct AcceptArgs {
   int64_t* out_tok; int64_t ot_st;
   int64_t* out_info; int64_t oi_st;
   int64_t* out_next; int64_t on_st;
+  const float* xtok;       // optional [T*M] draft-token logits under the parent (fused lm_head)
 };
 
 // Arguments of the accepted-path KV commit.
@@ -177,6 +178,29 @@ struct BundleArgs {
   int32_t* bundle_of;                      // optional [B, M] bundle of each node (-1: none)
 };
 
+// Arguments of the lm_head fused with the acceptance statistics.
+constexpr int kLmThreads = 256;            // 4 waves
+constexpr int kLmRB = 2;                   // 32-row vocabulary blocks per wave
+constexpr int kLmKS = 4;                   // 16-element MFMA sub-steps per step
+constexpr int kLmVocab = 128 * kLmRB;      // vocabulary rows per workgroup
+constexpr int kLmRows = 64;                // hidden rows per pass over W
+constexpr int kLmK = 16 * kLmKS;           // reduction elements per step
+struct LmArgs {
+  int mode;                                // 0 greedy, 1 typical
+  const uint16_t* h; int64_t ldh;          // [R, Dm] bf16 hidden rows (row t*M + i)
+  const uint16_t* w; int64_t ldw;          // [V, Dm] bf16 lm_head weight
+  int R, Dm;
+  int64_t V;
+  int T, M;
+  const int64_t* draft; int64_t d_st, d_sm;
+  const int64_t* parent; int64_t p_st, p_sm;
+  float inv_temp;
+  int nblk;                                // vocabulary blocks = partial statistics per row
+  float4* rstat; float* rstat2;            // [R, nblk] partial statistics
+  float* xtok;                             // [R] draft-token logits under the parent (typical)
+  uint16_t* lout; int64_t lo_sr;           // optional bf16 logits [R, V] (row stride)
+};
+
 // ---------------------------------------------------------------------------
 // Launchers (defined in the .hip files, called by the C-ABI layer).
 // ---------------------------------------------------------------------------
@@ -186,6 +210,14 @@ int attn_rows_per_block();
 int attn_blocks_per_cu();
 hipError_t launch_merge(const MergeArgs& a, hipStream_t s);
 hipError_t launch_accept(const AcceptArgs& a, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1);
+// Walk over per-row partial statistics part / part2 ([T*M, nin]) already
+// computed (fused lm_head): combines them into a.rstat / a.rstat2 (one per
+// row, a.nchunk == 1), then runs the walk.
+// lm_head + statistics, then the combine and the walk of kernel 4.
+hipError_t launch_lmhead_accept(const AcceptArgs& acc, const LmArgs& lm, hipStream_t s);
+int lmhead_blocks(int64_t V);
+hipError_t launch_accept_from_parts(const AcceptArgs& a, const float4* part, const float* part2, int nin,
+                                    hipStream_t s);
 hipError_t launch_commit(const CommitArgs& a, hipStream_t s);
 hipError_t launch_append(const AppendArgs& a, hipStream_t s);
 hipError_t launch_bundle_order(const BundleArgs& a, hipStream_t s);

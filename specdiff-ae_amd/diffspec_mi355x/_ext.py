@@ -72,6 +72,9 @@ SIGNATURES = {
     "dsv_kv_commit": (ctypes.c_int, [_P, _P, _I64, _P, _P, _I64, _V]),
     "dsv_kv_append": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _I64, _P, _P, _V]),
     "dsv_bundle_order": (ctypes.c_int, [_P, _I64, _I64, _I64, _P, _P, _V]),
+    "dsv_lmhead_accept_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, _I64]),
+    "dsv_lmhead_accept": (ctypes.c_int, [ctypes.c_int, _P, _P, _P, _P, _P, _I64, ctypes.c_float, ctypes.c_float,
+                                         ctypes.c_float, _P, _P, _P, _P, _P, _V, ctypes.c_size_t, _V]),
 }
 
 _lib: Optional[ctypes.CDLL] = None

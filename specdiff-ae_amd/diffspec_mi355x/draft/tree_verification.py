@@ -81,6 +81,60 @@ def tree_accept(logits: torch.Tensor, draft: torch.Tensor, parent: torch.Tensor,
     return out
 
 
+def lmhead_tree_accept(hidden: torch.Tensor, weight: torch.Tensor, draft: torch.Tensor, parent: torch.Tensor,
+                       pos: torch.Tensor, max_hops: int, mode: str = "greedy", temperature: float = 1.0,
+                       posterior_threshold: float = 0.09, posterior_alpha: float = 0.3,
+                       return_next: bool = False, return_logits: bool = False) -> Dict[str, torch.Tensor]:
+    """lm_head fused with the acceptance of T trees (kernel 5 + kernel 4's walk).
+
+    Same results as ``tree_accept(lm_head(hidden), ...)`` with bf16 logits
+    (the reference's ``self.base_model.lm_head`` output, draft/diffspec_model.py:229-231,
+    walked by draft/tree_verification.py:100-182), without writing the
+    ``[T, M, V]`` logits to memory.
+
+    Args:
+        hidden: [T, M, Dm] or [M, Dm] bf16 final hidden states of the tree nodes
+            (after the final norm); Dm a multiple of 64.
+        weight: [V, Dm] bf16 lm_head weight (``nn.Linear.weight``).
+        draft, parent, pos, max_hops, mode, ...: as :func:`tree_accept`.
+        return_logits: also write the bf16 logits ``[T, M, V]`` (returned as ``logits``).
+    """
+    if hidden.dim() == 2:
+        hidden = hidden.unsqueeze(0)
+    if draft.dim() == 1:
+        draft = draft.unsqueeze(0)
+    if parent.dim() == 1:
+        parent = parent.unsqueeze(0)
+    dev = _ext.require_gpu(hidden, weight, draft, parent, pos)
+    T, M, _ = hidden.shape
+    V = weight.shape[0]
+    if draft.dtype != torch.int64:
+        draft = draft.to(torch.int64)
+    if parent.dtype != torch.int64:
+        parent = parent.to(torch.int64)
+    if pos.dtype != torch.int64:
+        pos = pos.to(torch.int64)
+    mode_id = {"greedy": _ext.ACCEPT_GREEDY, "typical": _ext.ACCEPT_TYPICAL}[mode]
+    lib = _ext.load()
+    path = torch.empty((T, M), dtype=torch.int64, device=dev)
+    tokens = torch.empty((T, M), dtype=torch.int64, device=dev)
+    info = torch.empty((T, 4), dtype=torch.int64, device=dev)
+    nxt = torch.empty((T, M), dtype=torch.int64, device=dev) if return_next else None
+    logits = torch.empty((T, M, V), dtype=torch.bfloat16, device=dev) if return_logits else None
+    ws = _ext.workspace(lib.dsv_lmhead_accept_workspace_bytes(T, M, V), dev)
+    rc = lib.dsv_lmhead_accept(mode_id, _ext.desc(hidden), _ext.desc(weight), _ext.desc(draft), _ext.desc(parent),
+                               _ext.desc(pos), int(max_hops), float(temperature), float(posterior_threshold),
+                               float(posterior_alpha), _ext.desc(path), _ext.desc(tokens), _ext.desc(info),
+                               _ext.desc(nxt), _ext.desc(logits), ws.data_ptr(), ws.numel(), _ext.stream_of(dev))
+    _ext.check(rc, "lmhead_tree_accept")
+    out = {"path": path, "tokens": tokens, "info": info}
+    if return_next:
+        out["next"] = nxt
+    if return_logits:
+        out["logits"] = logits
+    return out
+
+
 def kv_commit(kv: torch.Tensor, start: int, path: torch.Tensor, info: torch.Tensor,
               page_table: Optional[torch.Tensor] = None, tree: int = 0) -> None:
     """Accepted-path KV commit on the GPU (reference draft/tree_verification.py:197-217).

@@ -1,0 +1,96 @@
+"""GPU parity of the lm_head fused with the acceptance (dsv_lmhead_accept).
+
+* logits: the fused kernel's bf16 logits (written on request) against the
+  fp64 oracle h . W^T rounded to bf16: within one bf16 step of the exactly
+  rounded value (fp32 accumulation), and equal for nearly all entries;
+* statistics and walk: bit-exact against kernel 4 run over those same logits
+  (greedy: argmax per node, path, tokens, info; typical: the same on seeded
+  cases), and next tokens equal to torch.argmax of those logits."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oa
+from diffspec_mi355x import workloads as wl
+from diffspec_mi355x.draft.tree_verification import lmhead_tree_accept, tree_accept
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(gpu, T, M, Dm, V, seed, sigma=0.1, max_depth=6):
+    g = torch.Generator().manual_seed(seed)
+    h = torch.randn((T, M, Dm), generator=g).to(torch.bfloat16).to(gpu)
+    w = (torch.randn((V, Dm), generator=g) * sigma).to(torch.bfloat16).to(gpu)
+    rng = np.random.default_rng(seed)
+    parents, depths = [], []
+    for t in range(T):
+        p, d = wl.make_tree(M, max_depth=max_depth, max_outdeg=4, seed=seed * 10 + t)
+        parents.append(p)
+        depths.append(d)
+    # plant a path of argmax tokens (torch fp32 logits) so that walks accept
+    ref = (h.float() @ w.float().T).argmax(-1).cpu().numpy()
+    draft = rng.integers(0, V, size=(T, M))
+    for t in range(T):
+        node = int(np.argmax(depths[t]))
+        while node > 0:
+            draft[t, node] = ref[t, parents[t][node]]
+            node = parents[t][node]
+    pref = torch.tensor([wl.parent_to_reference(p) for p in parents], dtype=torch.int64, device=gpu)
+    pos = torch.tensor([[100 + x for x in d] for d in depths], dtype=torch.int64, device=gpu)
+    return h, w, torch.from_numpy(draft).to(gpu), pref, pos, max_depth
+
+
+def _check_logits(h, w, lg):
+    hd, wd = h.double().cpu().numpy(), w.double().cpu().numpy()
+    exact = hd @ wd.T
+    want = oa.bf16_round(exact.astype(np.float32))
+    got = lg.float().cpu().numpy()
+    # one bf16 step (8 significant bits) at the larger magnitude, plus the
+    # fp32 accumulation error sqrt(Dm) * 2^-24 * sum |h w| (x4), which
+    # matters where the sum cancels to a small value
+    mag = np.maximum(np.maximum(np.abs(got), np.abs(want)), 1e-30)
+    ulp = np.exp2(np.floor(np.log2(mag)) - 7)
+    acc = 4 * np.sqrt(hd.shape[1]) * 2.0 ** -24 * (np.abs(hd) @ np.abs(wd).T)
+    diff = np.abs(got - want)
+    assert np.all(diff <= ulp + acc), float((diff / (ulp + acc)).max())
+    assert np.mean(diff == 0) > 0.98
+
+
+@pytest.mark.parametrize("T,M,Dm,V", [(1, 64, 512, 5000), (2, 20, 128, 1000), (3, 40, 256, 3000), (1, 1, 64, 300)])
+@pytest.mark.parametrize("mode", ["greedy", "typical"])
+def test_fused_matches_kernel4_on_its_logits(gpu, T, M, Dm, V, mode):
+    print(f"[lmhead] T={T} M={M} Dm={Dm} V={V} mode={mode}", flush=True)
+    h, w, draft, pref, pos, md = _case(gpu, T, M, Dm, V, seed=T * 7 + M)
+    hops = min(md + 2, M)
+    r = lmhead_tree_accept(h, w, draft, pref, pos, hops, mode=mode, return_next=True, return_logits=True)
+    torch.cuda.synchronize()
+    lg = r["logits"]
+    _check_logits(h.reshape(T * M, Dm), w, lg.reshape(T * M, V))
+    ref = tree_accept(lg, draft, pref, pos, hops, mode=mode, return_next=True)
+    torch.cuda.synchronize()
+    assert torch.equal(r["next"], ref["next"])
+    assert torch.equal(r["next"], lg.argmax(-1))
+    assert torch.equal(r["info"], ref["info"])
+    assert torch.equal(r["path"], ref["path"]) and torch.equal(r["tokens"], ref["tokens"])
+    if M > 1:
+        assert int(r["info"][:, 1].max()) >= 1   # the planted paths are (at least partly) accepted
+
+
+def test_without_logits_output_and_llama_shape(gpu):
+    # Llama-3.1-8B lm_head: Dm 4096, V 128256; 64 nodes.  The logits are
+    # checked on a vocabulary subset against the fp64 oracle.
+    T, M, Dm, V = 1, 64, 4096, 128256
+    h, w, draft, pref, pos, md = _case(gpu, T, M, Dm, V, seed=11, sigma=0.02)
+    hops = min(md + 2, M)
+    r1 = lmhead_tree_accept(h, w, draft, pref, pos, hops, return_next=True)
+    r2 = lmhead_tree_accept(h, w, draft, pref, pos, hops, return_next=True, return_logits=True)
+    torch.cuda.synchronize()
+    lg = r2["logits"]
+    for k in ("next", "info", "path", "tokens"):
+        assert torch.equal(r1[k], r2[k])
+    ref = tree_accept(lg, draft, pref, pos, hops, return_next=True)
+    torch.cuda.synchronize()
+    assert torch.equal(r1["next"], ref["next"]) and torch.equal(r1["info"], ref["info"])
+    cols = torch.from_numpy(np.random.default_rng(0).choice(V, 3000, replace=False)).to(gpu)
+    _check_logits(h[0], w[cols], lg[0][:, cols])
