@@ -1068,6 +1068,7 @@ int dsv_tree_accept(int mode, const dsv_tensor* logits, const dsv_tensor* draft,
   const size_t rows = (size_t)T * M * a.nchunk;
   a.rstat = static_cast<float4*>(workspace);
   a.rstat2 = reinterpret_cast<float*>(static_cast<char*>(workspace) + align_up(rows * 16, 256));
+  if (g_dry_run) return DSV_OK;
   hipEvent_t ev0, ev1;
   take_events(ev0, ev1);
   hipError_t e = dsv::launch_accept(a, static_cast<hipStream_t>(stream), ev0, ev1);

@@ -187,6 +187,48 @@ def test_bundle_order_validation(dsv_lib):
     assert rc == 0
 
 
+def test_lmhead_accept_validation(dsv_lib):
+    none = _ext.DsvTensor()
+    T, M, Dm, V = 1, 8, 96, 500
+    hidden = _t((T, M, Dm))
+    weight = _t((V, Dm))
+    draft, parent, pos = _t((T, M), _ext.DSV_I64), _t((T, M - 1), _ext.DSV_I64), _t((T, M), _ext.DSV_I64)
+    outs = [_t((T, M), _ext.DSV_I64), _t((T, M), _ext.DSV_I64), _t((T, 4), _ext.DSV_I64)]
+
+    def call(h, w, ws_bytes=1 << 20, lo=none):
+        return dsv_lib.dsv_lmhead_accept(0, ctypes.byref(h), ctypes.byref(w), ctypes.byref(draft), ctypes.byref(parent),
+                                         ctypes.byref(pos), 4, 1.0, 0.09, 0.3, ctypes.byref(outs[0]),
+                                         ctypes.byref(outs[1]), ctypes.byref(outs[2]), ctypes.byref(none),
+                                         ctypes.byref(lo), ctypes.c_void_p(0x100000), ws_bytes, None)
+
+    rc = call(hidden, weight)  # Dm = 96 is not a multiple of 64
+    assert rc == -2 and "multiple of 64" in _ext.last_error()
+    Dm = 128
+    hidden, weight = _t((T, M, Dm)), _t((V, Dm))
+    rc = call(hidden, _t((V, 64)))
+    assert rc == -1 and "weight must be" in _ext.last_error()
+    rc = call(hidden, weight, ws_bytes=16)
+    assert rc == -3 and "workspace" in _ext.last_error()
+    rc = call(hidden, weight, lo=_t((T, M, V + 1)))
+    assert rc == -1 and "logits_out" in _ext.last_error()
+    need = dsv_lib.dsv_lmhead_accept_workspace_bytes(T, M, V)
+    assert need > 0
+    dsv_lib.dsv_set_dry_run(1)
+    try:
+        assert call(hidden, weight, ws_bytes=need, lo=_t((T, M, V))) == 0
+        # a root-only tree: its parent tensor is empty and may have no storage
+        h1 = _t((T, 1, Dm))
+        d1, p1, q1 = _t((T, 1), _ext.DSV_I64), _t((T, 0), _ext.DSV_I64, ptr=0), _t((T, 1), _ext.DSV_I64)
+        o1 = [_t((T, 1), _ext.DSV_I64), _t((T, 1), _ext.DSV_I64), _t((T, 4), _ext.DSV_I64)]
+        rc = dsv_lib.dsv_lmhead_accept(1, ctypes.byref(h1), ctypes.byref(weight), ctypes.byref(d1), ctypes.byref(p1),
+                                       ctypes.byref(q1), 2, 1.0, 0.09, 0.3, ctypes.byref(o1[0]), ctypes.byref(o1[1]),
+                                       ctypes.byref(o1[2]), ctypes.byref(none), ctypes.byref(none),
+                                       ctypes.c_void_p(0x100000), need, None)
+        assert rc == 0, _ext.last_error()
+    finally:
+        dsv_lib.dsv_set_dry_run(0)
+
+
 def test_python_api_refuses_cpu_tensors(dsv_lib):
     from diffspec_mi355x.runtime.tree_attention import prefix_attention_forward, tree_verify
     from diffspec_mi355x.draft.tree_verification import tree_accept
