@@ -35,6 +35,7 @@
 // attention), runtime/bundle_verifier.py:26-135 (masked bundle attention).
 
 #include "dsv_attn_geo.h"
+#include "dsv_dma.h"
 #include "dsv_internal.h"
 
 namespace dsv {
@@ -47,7 +48,6 @@ constexpr float kNegInf = -__builtin_huge_valf();
 constexpr float kRescaleTau = 8.0f;
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 template <typename T>
@@ -96,9 +96,6 @@ __device__ __forceinline__ int64_t load_index(const void* p, int is64, int64_t i
   return is64 ? reinterpret_cast<const int64_t*>(p)[i] : (int64_t) reinterpret_cast<const int32_t*>(p)[i];
 }
 
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
 
 // LDS-DMA: 16 bytes per lane, lane l lands at LDS m0 + 16*l.  K/V bytes are
 // read once per verify step: the loads are marked non-temporal (nt).
@@ -114,47 +111,12 @@ __device__ __forceinline__ void dma_buf(uint32_t lds, const void* base, uint32_t
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds" ::"s"(m0), "v"(voff), "s"(r)
                : "memory", "m0");
 }
-// A buffer resource (base, byte range) in SGPRs, built once and reused.
-__device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t range) {
-  const uint64_t p = (uint64_t)base;
-  i32x4 r;
-  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)p);
-  r[1] = __builtin_amdgcn_readfirstlane((int)(uint32_t)(p >> 32));
-  r[2] = __builtin_amdgcn_readfirstlane((int)range);
-  r[3] = 0x00020000;
-  return r;
-}
-__device__ __forceinline__ void dma_rs(uint32_t lds, i32x4 r_in, uint32_t voff) {
-  // Uniform by construction; readfirstlane keeps the resource in SGPRs where
-  // the compiler cannot prove it (free when it already is).
-  i32x4 r;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) r[i] = __builtin_amdgcn_readfirstlane(r_in[i]);
-  const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds" ::"s"(m0), "v"(voff), "s"(r)
-               : "memory", "m0");
-}
 // With a full per-lane address (keys clamped to valid ones by the caller).
 __device__ __forceinline__ void dma_lane(uint32_t lds, const void* vaddr) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds);
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off nt" ::"s"(m0), "v"(vaddr) : "memory", "m0");
 }
 
-// Wait until at most N of this wave's vector-memory operations are pending.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-// Workgroup barrier that the compiler may not move LDS accesses across and
-// that adds no memory-counter waits of its own (the DMA loads are waited for
-// explicitly with wait_vmcnt before it).
-__device__ __forceinline__ void barrier_lds() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
 
 // Does element (i, j) of a dense tree-mask block keep the key?
 __device__ __forceinline__ bool tmask_keep(const AttnArgs& a, int b, int i, int j) {

@@ -57,7 +57,8 @@ def _check_logits(h, w, lg):
     assert np.mean(diff == 0) > 0.98
 
 
-@pytest.mark.parametrize("T,M,Dm,V", [(1, 64, 512, 5000), (2, 20, 128, 1000), (3, 40, 256, 3000), (1, 1, 64, 300)])
+@pytest.mark.parametrize("T,M,Dm,V", [(1, 64, 512, 5000), (2, 20, 128, 1000), (3, 40, 256, 3000), (1, 1, 64, 300),
+                                       (1, 5, 192, 700), (2, 3, 320, 260)])
 @pytest.mark.parametrize("mode", ["greedy", "typical"])
 def test_fused_matches_kernel4_on_its_logits(gpu, T, M, Dm, V, mode):
     print(f"[lmhead] T={T} M={M} Dm={Dm} V={V} mode={mode}", flush=True)
