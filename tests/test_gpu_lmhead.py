@@ -95,3 +95,24 @@ def test_without_logits_output_and_llama_shape(gpu):
     assert torch.equal(r1["next"], ref["next"]) and torch.equal(r1["info"], ref["info"])
     cols = torch.from_numpy(np.random.default_rng(0).choice(V, 3000, replace=False)).to(gpu)
     _check_logits(h[0], w[cols], lg[0][:, cols])
+
+
+def test_strided_hidden_temperature_and_shared_positions(gpu):
+    # hidden rows at a padded stride (a [T, M, Dm] view of a wider buffer),
+    # typical acceptance at temperature 0.7, one [M] position row for all trees
+    T, M, Dm, V = 2, 24, 256, 2000
+    h, w, draft, pref, pos, md = _case(gpu, T, M, Dm, V, seed=23)
+    wide = torch.zeros((T, M, Dm + 64), dtype=torch.bfloat16, device=gpu)
+    wide[..., :Dm] = h
+    hv = wide[..., :Dm]
+    assert hv.stride(1) == Dm + 64
+    pos1 = pos[0]
+    hops = min(md + 2, M)
+    r = lmhead_tree_accept(hv, w, draft, pref, pos1, hops, mode="typical", temperature=0.7, return_next=True,
+                           return_logits=True)
+    torch.cuda.synchronize()
+    _check_logits(h.reshape(T * M, Dm), w, r["logits"].reshape(T * M, V))
+    ref = tree_accept(r["logits"], draft, pref, pos1, hops, mode="typical", temperature=0.7, return_next=True)
+    torch.cuda.synchronize()
+    for k in ("next", "info", "path", "tokens"):
+        assert torch.equal(r[k], ref[k]), k
