@@ -205,13 +205,22 @@ def bench_config3(args, lib, ev):
     host_us = (time.perf_counter() - t0) / reps * 1e6
     nb = algorithmic_bytes(N, M, H, Hk, D)
     flops = 4 * M * H * N * D + 4 * M * H * M * D
+    # the tree block counted over visible keys only: 4*H*D * sum_i |anc(i)|
+    anc = [0] * M
+    for i in range(M):
+        j, c = i, 0
+        while j >= 0 and c <= M:
+            c += 1
+            j = inp.parent[j] if j > 0 else -1
+        anc[i] = c
+    flops_masked = 4 * M * H * N * D + 4 * H * D * sum(anc)
     return {"workload": "tree-verify attention, N=131072, M=128 (8 bundles, row-packed), paged bf16 KV, "
                         f"{layers} KV layers rotated", "us_per_step": round(us_step, 3),
             "kernel1_avg_us": round(k1_us, 3), "kernel1_tflops": round(flops / (k1_us * 1e-6) / 1e12, 1),
             "kernel1_mfma_frac": round(flops / (k1_us * 1e-6) / 2.5e15, 4),
             "kernel1_hbm_gbs": round(nb["kernel1"] / (k1_us * 1e-6) / 1e9, 1),
             "kernel1_hbm_frac": round(nb["kernel1"] / (k1_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-            "flops_dense": flops, "bytes_per_launch": nb["kernel1"],
+            "flops_dense": flops, "flops_masked": flops_masked, "bytes_per_launch": nb["kernel1"],
             "bundle_order": {"device_us": round(order_us, 2),
                              "host_scheduler_us": round(host_us, 1),
                              "timing": "device: HIP graph replay; host: parent to host, Python "
@@ -355,7 +364,9 @@ def bench_config5(args, lib, ev):
             "attention_us_per_step": round(attn_us, 1), "attention_share": round(attn_us / us_step, 3),
             "weight_bytes": wbytes, "kv_bytes": kvbytes,
             "hbm_gbs": round((wbytes + kvbytes) / (us_step * 1e-6) / 1e9, 1),
-            "accept_length": int(r["info"][0, 1]), "kv_commit": commit,
+            "accept_length": int(r["info"][0, 1]),
+            "tokens_per_s": round((int(r["info"][0, 1]) + 1) / (us_step * 1e-6), 1),
+            "lmhead_accept_share": round(lmh["fused_us"] / us_step, 4), "kv_commit": commit,
             "kv_append_one_layer": dict(app, bytes=(M * (H + 2 * Hk) * D * 2) * 2), "lmhead_accept": lmh}
 
 
