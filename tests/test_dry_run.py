@@ -124,7 +124,11 @@ def pool_half(pool, layer, kv):
     (1000, 16, 16, 32, 8, 128, False),
     # per-lane DMA mode: pages smaller than a DMA instruction, unaligned tree start
     (1000, 64, 2, 32, 8, 128, False), (101, 33, 16, 32, 8, 128, False), (777, 20, 4, 16, 4, 64, False),
-    (50, 9, 1, 8, 2, 128, False)])
+    (50, 9, 1, 8, 2, 128, False),
+    # the page sizes of tests/test_gpu_attention.py::test_tree_verify_page_sizes
+    (1000, 64, 1, 8, 2, 128, False), (1000, 64, 2, 8, 2, 128, False), (1000, 64, 4, 8, 2, 64, False),
+    (1000, 64, 8, 8, 2, 128, False), (1000, 64, 32, 8, 2, 128, True), (1000, 64, 64, 8, 2, 128, False),
+    (5000, 48, 256, 8, 2, 128, False)])
 def test_tree_verify_paged_and_dense(dry, n_prefix, M, ps, H, Hk, D, perm):
     a = Alloc()
     B = 1

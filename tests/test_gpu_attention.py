@@ -147,6 +147,27 @@ def test_tree_verify_paged_matches_oracle(gpu, n_prefix, M):
     assert_lse_close(np64(lse[0]), l_ref)
 
 
+@pytest.mark.parametrize("ps,D,n_prefix,M", [(1, 128, 1000, 64), (2, 128, 1000, 64), (4, 64, 1000, 64),
+                                             (8, 128, 1000, 64), (32, 128, 1000, 64), (64, 128, 1000, 64),
+                                             (256, 128, 5000, 48)])
+def test_tree_verify_page_sizes(gpu, ps, D, n_prefix, M):
+    # Pages smaller than one DMA instruction (per-lane addresses), and pages
+    # larger than a tile: bit-equal to the dense cache holding the same
+    # logical tokens, and within tolerance of the oracle.
+    print(f"[tree_verify page size] ps={ps} D={D} n_prefix={n_prefix} M={M}", flush=True)
+    inp = wl.make_tree_verify_inputs(n_prefix=n_prefix, M=M, H=8, Hk=2, D=D, page_size=ps, seed=ps, tree_seed=ps,
+                                     device=str(gpu))
+    par = torch.tensor(inp.parent, dtype=torch.int64, device=gpu)
+    o_p, l_p = tree_verify(inp.q, inp.kv_pages[0, 0], inp.kv_pages[0, 1], n_prefix, par, page_table=inp.page_table)
+    kc, vc = inp.logical_kv(0, 0).contiguous(), inp.logical_kv(0, 1).contiguous()
+    o_d, l_d = tree_verify(inp.q, kc, vc, n_prefix, par)
+    torch.cuda.synchronize()
+    assert torch.equal(o_p, o_d) and torch.equal(l_p, l_d)
+    o_ref, l_ref = oracle_tree_verify(inp)
+    assert_attn_close(np64(o_p[0]), o_ref)
+    assert_lse_close(np64(l_p[0]), l_ref)
+
+
 def test_tree_verify_dense_equals_paged_and_perm_invariant(gpu):
     inp = paged_case(gpu, 3000, 64, tree_seed=5)
     par = torch.tensor(inp.parent, dtype=torch.int32, device=gpu)
