@@ -202,3 +202,29 @@ def test_inconsistent_shapes_are_rejected_before_any_access(dry):
     rc = dry.dsv_prefix_attention_forward(ctypes.byref(q), ctypes.byref(k_short), ctypes.byref(v), -1,
                                           ctypes.byref(out), ctypes.byref(lse), wsp, ws, None)
     assert rc == -1 and "shapes differ" in _ext.last_error()
+
+
+@pytest.mark.parametrize("ps", [16, 4])
+def test_tree_verify_batched_page_table(dry, ps):
+    # the shape of tests/test_gpu_attention.py::test_tree_verify_batched_paged_f16:
+    # B = 2, one page-table row per batch (int64), f16, a parent row per batch
+    a = Alloc()
+    B, M, H, Hk, D, n_prefix = 2, 40, 8, 2, 128, 700
+    n_pages = (n_prefix + M + ps - 1) // ps
+    q = tensor(a, (B, M, H, D), _ext.DSV_F16)
+    pool = tensor(a, (1, 2, B * n_pages, Hk, ps, D), _ext.DSV_F16)
+    pt = tensor(a, (B, n_pages), _ext.DSV_I64)
+    par = tensor(a, (B, M), _ext.DSV_I64)
+    out, lse = tensor(a, (B, M, H, D), _ext.DSV_F16), tensor(a, (B, M, H), _ext.DSV_F32)
+    ws = dry.dsv_attn_workspace_bytes(B, M, H, Hk, D, n_prefix, ps, 1)
+    kh, vh = pool_half(pool, 0, 0), pool_half(pool, 0, 1)
+    rc = dry.dsv_tree_verify(ctypes.byref(q), ctypes.byref(kh), ctypes.byref(vh), ctypes.byref(pt), n_prefix,
+                             ctypes.byref(par), ctypes.byref(none()), ctypes.byref(out), ctypes.byref(lse), a.take(ws),
+                             ws, None)
+    ok(dry, rc, "tree_verify batched page table")
+    kc, vc = tensor(a, (B, n_prefix + M, Hk, D), _ext.DSV_F16), tensor(a, (B, n_prefix + M, Hk, D), _ext.DSV_F16)
+    ws2 = dry.dsv_attn_workspace_bytes(B, M, H, Hk, D, n_prefix, 0, 1)
+    rc = dry.dsv_tree_verify(ctypes.byref(q), ctypes.byref(kc), ctypes.byref(vc), ctypes.byref(none()), n_prefix,
+                             ctypes.byref(par), ctypes.byref(none()), ctypes.byref(out), ctypes.byref(lse), a.take(ws2),
+                             ws2, None)
+    ok(dry, rc, "tree_verify batched dense")

@@ -168,6 +168,34 @@ def test_tree_verify_page_sizes(gpu, ps, D, n_prefix, M):
     assert_lse_close(np64(l_p[0]), l_ref)
 
 
+@pytest.mark.parametrize("ps", [16, 4])
+def test_tree_verify_batched_paged_f16(gpu, ps):
+    # B = 2 with one int64 page-table row per batch over one shared pool, a
+    # different tree per batch, f16 end to end.
+    print(f"[tree_verify batched paged f16] ps={ps}", flush=True)
+    B, M, H, Hk, D, n_prefix = 2, 40, 8, 2, 128, 700
+    n_tok = n_prefix + M
+    n_pages = (n_tok + ps - 1) // ps
+    q = rand((B, M, H, D), 31, torch.float16, gpu)
+    pool = rand((1, 2, B * n_pages, Hk, ps, D), 32, torch.float16, gpu)
+    perm = np.random.default_rng(ps).permutation(B * n_pages).astype(np.int64).reshape(B, n_pages)
+    pt = torch.from_numpy(perm).to(gpu)
+    parents = [wl.make_tree(M, max_depth=6, max_outdeg=4, seed=40 + b)[0] for b in range(B)]
+    par = torch.tensor(parents, dtype=torch.int64, device=gpu)
+    o_p, l_p = tree_verify(q, pool[0, 0], pool[0, 1], n_prefix, par, page_table=pt)
+    tok = torch.arange(n_tok, device=gpu)
+    kc = torch.stack([pool[0, 0][pt[b][tok // ps], :, tok % ps] for b in range(B)]).contiguous()
+    vc = torch.stack([pool[0, 1][pt[b][tok // ps], :, tok % ps] for b in range(B)]).contiguous()
+    o_d, l_d = tree_verify(q, kc, vc, n_prefix, par)
+    torch.cuda.synchronize()
+    assert o_p.dtype == torch.float16
+    assert torch.equal(o_p, o_d) and torch.equal(l_p, l_d)
+    for b in range(B):
+        o_ref, l_ref = oa.tree_verify(np64(q[b]), np64(kc[b]), np64(vc[b]), n_prefix, parents[b])
+        assert_attn_close(np64(o_p[b]), o_ref, what=f"b={b}")
+        assert_lse_close(np64(l_p[b]), l_ref, what=f"b={b}")
+
+
 def test_tree_verify_dense_equals_paged_and_perm_invariant(gpu):
     inp = paged_case(gpu, 3000, 64, tree_seed=5)
     par = torch.tensor(inp.parent, dtype=torch.int32, device=gpu)
