@@ -86,6 +86,49 @@ def test_prefix_attention_expanded_kv_and_cache_seqlens(gpu):
     assert_lse_close(np64(l3[0]), l_ref)
 
 
+def rising_scores_case(profile, B, M, H, Hk, D, N, seed=11):
+    """q, k whose scores grow along the key sequence (in nats, after the 1/sqrt(D) scale).
+
+    saw: the scores rise from about 0 to about 60 over every 64 keys (two 32-key tiles)
+    and drop back, so inside any run of keys that starts on a multiple of 64 the row
+    maximum jumps by about 30 nats from the first tile to the second.
+    late_spike: small scores except a few keys near the end whose scores are about 60
+    nats above the rest.
+    """
+    g = torch.Generator().manual_seed(seed)
+    G = H // Hk
+    u = torch.where(torch.rand((Hk, D), generator=g) < 0.5, -1.0, 1.0)  # |u|^2 = D
+    q = 0.3 * torch.randn((B, M, H, D), generator=g) + 4.0 * u.repeat_interleave(G, dim=0)[None, None]
+    k = 0.3 * torch.randn((B, N, Hk, D), generator=g)
+    v = torch.randn((B, N, Hk, D), generator=g)
+    s = 4.0 * D / D ** 0.5  # score of k = u against q = 4u
+    if profile == "saw":
+        alpha = (60.0 / s) * (torch.arange(N) % 64).float() / 63.0
+        k = k + alpha[None, :, None, None] * u[None, None]
+    else:
+        for n in (N - 40, N - 7, N - 1):
+            k[:, n] += (60.0 / s) * u[None]
+    return q, k, v
+
+
+@pytest.mark.parametrize("profile,N", [("saw", 3000), ("saw", 20000), ("late_spike", 3000)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_prefix_attention_rising_scores(gpu, profile, N, dtype):
+    """Row maxima that jump by tens of nats from one tile to the next inside a split:
+    the online softmax must follow them (the accumulators hold the full range without
+    overflow)."""
+    B, M, H, Hk, D = 1, 24, 16, 4, 128
+    print(f"[rising] profile={profile} N={N} dtype={dtype}", flush=True)
+    q, k, v = (x.to(dtype).to(gpu) for x in rising_scores_case(profile, B, M, H, Hk, D, N))
+    out, lse = prefix_attention_forward(q, k, v, B, M, H, D)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all() and torch.isfinite(lse).all()
+    o_ref, l_ref = oa.prefix_attention(np64(q[0]), np64(k[0]), np64(v[0]))
+    assert l_ref.min() > 40.0  # every row's maximum lies > 40 nats above its first keys' scores
+    assert_attn_close(np64(out[0]), o_ref)
+    assert_lse_close(np64(lse[0]), l_ref)
+
+
 @pytest.mark.parametrize("mask_kind", ["float_additive", "int8", "bool", "bf16_additive"])
 def test_tree_attention_forward_matches_oracle(gpu, mask_kind):
     B, M, H, Hk, D, T = 2, 64, 32, 8, 128, 70
