@@ -153,7 +153,7 @@ def bench_verify(args, lib, ev):
     return inp, total_ms / args.steps, k1_ms, t_wall, se0.elapsed_time(se1) / args.steps
 
 
-def bench_config3(args, lib, ev):
+def bench_bundle_packed_128k(args, lib, ev):
     """128K paged prefix, 128-node tree (depth <= 12, out-degree <= 6), query
     rows packed in bundle order (8 bundles).  MFMA-bound: 512 flop/B.  A step
     computes the bundle order on the GPU from the device parent array
@@ -249,7 +249,7 @@ def device_us(fn, calls=10, reps=20):
     return e0.elapsed_time(e1) / (reps * calls) * 1e3
 
 
-def bench_config5(args, lib, ev):
+def bench_llama8b_step(args, lib, ev):
     """One verify step of a Llama-3.1-8B-shaped target (32 layers, hidden 4096,
     32/8 heads, FFN 14336, vocab 128256, RoPE theta 5e5) over a 64-node tree
     with a 65536-token paged prefix per layer, random N(0, 0.02) bf16 weights.
@@ -493,7 +493,7 @@ def cpu_baseline(inp, args):
         if len(times) >= args.cpu_max_steps:
             break
     return {"value": statistics.median(times) * 1e6, "unit": "us/verify-step", "cores": cores, "kind": "port",
-            "sample": f"{len(times)} full config-2 verify steps (1 layer, N={n_prefix}, M={M}, fp32 upcast), "
+            "sample": f"{len(times)} full verify steps (1 layer, N={n_prefix}, M={M}, fp32 upcast), "
                       f"median"}, out
 
 
@@ -511,8 +511,8 @@ def main():
     ap.add_argument("--cpu-max-steps", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-accept", action="store_true")
-    ap.add_argument("--no-config3", action="store_true")
-    ap.add_argument("--no-config5", action="store_true")
+    ap.add_argument("--no-bundle-128k", action="store_true")
+    ap.add_argument("--no-llama-step", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy (scale reference for the FETCH_SIZE / WRITE_SIZE "
                          "counters) and exit")
@@ -573,12 +573,12 @@ def main():
                                "the dispatch latency)", "us_per_step_in_that_pass": round(ms_step_ev * 1e3, 3)},
         "wall_s_timed": round(t_wall, 4),
     }
-    if not args.no_config3:
-        print("[bench] config 3 (N=131072, M=128)", file=sys.stderr, flush=True)
-        line["config3"] = bench_config3(args, lib, ev)
-    if not args.no_config5:
-        print("[bench] config 5 (32-layer verify step)", file=sys.stderr, flush=True)
-        line["config5"] = bench_config5(args, lib, ev)
+    if not args.no_bundle_128k:
+        print("[bench] bundle-packed verify (N=131072, M=128)", file=sys.stderr, flush=True)
+        line["bundle_packed_128k"] = bench_bundle_packed_128k(args, lib, ev)
+    if not args.no_llama_step:
+        print("[bench] Llama-3.1-8B-shaped verify step (32 layers)", file=sys.stderr, flush=True)
+        line["llama8b_verify_step"] = bench_llama8b_step(args, lib, ev)
     if not args.no_accept:
         print("[bench] acceptance kernel", file=sys.stderr, flush=True)
         line["acceptance"] = bench_accept(args, lib, ev)

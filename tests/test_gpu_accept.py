@@ -36,8 +36,8 @@ def run_and_compare(logits, draft, parent_ref, pos, max_depth, mode="greedy", **
 
 
 @pytest.mark.parametrize("mode", ["greedy", "typical"])
-def test_config4_bit_exact(gpu, mode):
-    """Config 4: 8 trees x 64 nodes, bf16 logits [8, 64, 128256] N(0, 3) with a
+def test_accept_8x64_vocab128256_bit_exact(gpu, mode):
+    """8 trees x 64 nodes, bf16 logits [8, 64, 128256] N(0, 3) with a
     planted top token per node and a planted path of length 1..8."""
     a = wl.make_accept_inputs(T=8, M=64, V=128256, device=str(gpu), pos_offset=1000)
     kw = dict(temperature=1.0, posterior_threshold=0.09, posterior_alpha=0.3) if mode == "typical" else {}

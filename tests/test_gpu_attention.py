@@ -307,8 +307,8 @@ def test_verify_bundle_fully_masked_row_and_paged_equivalence(gpu):
     assert_lse_close(np64(l_p[0]), l_ref)
 
 
-def test_config1_fp32_inputs_within_north_star_tolerance(gpu):
-    """Config 1 shapes (N=4096, M=64, GQA 32/8, D=128, N(0,1) fp32, seed 0): the
+def test_fp32_inputs_4k_ctx_within_tolerance(gpu):
+    """N=4096, M=64, GQA 32/8, D=128, N(0,1) fp32, seed 0): the
     kernels take bf16, so the fp32 inputs are rounded on the host; the result
     is compared with the fp32-input oracle."""
     g = torch.Generator().manual_seed(0)
@@ -328,8 +328,8 @@ def test_config1_fp32_inputs_within_north_star_tolerance(gpu):
     assert_lse_close(np64(lse[0]), l_ref, tol=5e-2)
 
 
-def test_config2_full_size_subset_heads(gpu):
-    """Config 2: 64K paged prefix, 64-node tree, bf16 N(0,1)*0.5; heads of KV heads 0-1 vs oracle."""
+def test_64k_ctx_64_nodes_subset_heads(gpu):
+    """64K paged prefix, 64-node tree, bf16 N(0,1)*0.5; heads of KV heads 0-1 vs oracle."""
     inp = paged_case(gpu, 65536, 64)
     par = torch.tensor(inp.parent, dtype=torch.int64, device=gpu)
     out, lse = tree_verify(inp.q, inp.kv_pages[0, 0], inp.kv_pages[0, 1], 65536, par, page_table=inp.page_table,
@@ -351,8 +351,8 @@ def test_config2_full_size_subset_heads(gpu):
     assert_lse_close(np64(lse_t[0, :, :8]), l_t)
 
 
-def test_config3_bundle_packed_subset_heads(gpu):
-    """Config 3: 128K paged prefix, 128-node tree (depth <= 12, out-degree <= 6),
+def test_128k_ctx_128_nodes_bundle_packed_subset_heads(gpu):
+    """128K paged prefix, 128-node tree (depth <= 12, out-degree <= 6),
     query rows packed in bundle order (8 bundles); KV head 0 vs oracle."""
     inp = paged_case(gpu, 131072, 128, seed=2, tree_seed=2, max_depth=12, max_outdeg=6)
     par = torch.tensor(inp.parent, dtype=torch.int64, device=gpu)

@@ -166,7 +166,7 @@ def test_bf16_round_matches_torch():
 
 def test_oracle_matches_reference_cpu_op_sequence():
     """The closed form agrees with the reference's own CPU path (prefix
-    fallback + naive tree + sigmoid merge) on a config-1-like case (fp32)."""
+    fallback + naive tree + sigmoid merge) on a small fp32 case."""
     torch.manual_seed(0)
     B, M, H, Hk, D, N = 1, 16, 8, 2, 32, 200
     q = torch.randn(B, M, H, D)
