@@ -977,6 +977,7 @@ static int accept_common(int mode, int64_t T, int64_t M, int64_t V, const dsv_te
                          dsv_tensor* out_tokens, dsv_tensor* out_info, dsv_tensor* out_next, dsv::AcceptArgs& a) {
   int rc;
   if (M < 1 || M > 1024) return fail(DSV_ERR_UNSUPPORTED, "trees of %lld nodes are not supported (1..1024)", (long long)M);
+  if (T < 1 || T > (1 << 20)) return fail(DSV_ERR_INVALID, "tree count %lld out of range (1..2^20)", (long long)T);
   if (V < 1 || V > 0x7fffffff) return fail(DSV_ERR_INVALID, "vocab size out of range");
   if ((rc = check_nd(draft, "draft", 2)) != DSV_OK) return rc;
   if (draft->dtype != DSV_I64 || draft->shape[0] != T || draft->shape[1] != M)

@@ -101,6 +101,13 @@ def test_accept_validation(dsv_lib):
                                  ctypes.byref(pos), 10, 1.0, 0.09, 0.3, ctypes.byref(o), ctypes.byref(o),
                                  ctypes.byref(info), ctypes.byref(none), None, 0, None)
     assert rc == -1 and "mode" in _ext.last_error()
+    # no trees at all: rejected, not launched with an empty grid
+    logits0, draft0 = _t((0, 8, 100), _ext.DSV_BF16), _t((0, 8), _ext.DSV_I64)
+    parent0, o0, info0 = _t((0, 7), _ext.DSV_I64), _t((0, 8), _ext.DSV_I64), _t((0, 4), _ext.DSV_I64)
+    rc = dsv_lib.dsv_tree_accept(0, ctypes.byref(logits0), ctypes.byref(draft0), ctypes.byref(parent0),
+                                 ctypes.byref(pos), 10, 1.0, 0.09, 0.3, ctypes.byref(o0), ctypes.byref(o0),
+                                 ctypes.byref(info0), ctypes.byref(none), None, 0, None)
+    assert rc == -1 and "tree count" in _ext.last_error()
 
 
 def test_kv_commit_validation(dsv_lib):
