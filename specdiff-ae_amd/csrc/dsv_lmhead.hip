@@ -19,10 +19,12 @@
 //     64 elements of Dm in flight ahead of the MFMAs);
 //   * the hidden rows (B operand, 64 rows x 64 elements per step) are staged
 //     once per workgroup through a double-buffered LDS tile;
-//   * v_mfma_f32_32x32x16_bf16, 16 per wave per step.  A lane reads 64
-//     contiguous bytes of its W row per step, and the MFMA k slots map onto
-//     that run: lanes 0-31 carry elements [0, 32) of the step, lanes 32-63
-//     elements [32, 64), in four 8-element MFMA steps, the same on A and B.
+//   * v_mfma_f32_32x32x16_bf16, 16 per wave per step.  MFMA sub-step j of a
+//     step covers elements [16j, 16j + 16) of the step's 64: lanes 0-31 hold
+//     the first 8, lanes 32-63 the next 8, the same on A and B, so one load
+//     instruction reads 32 contiguous bytes of each of 32 W rows;
+//   * workgroups start their sweep over Dm at different steps (a rotation),
+//     which spreads their concurrent W reads over the memory channels.
 // Hidden rows beyond R are zero; vocabulary rows beyond V are clamped loads
 // whose results are dropped.
 
