@@ -75,7 +75,8 @@ def ok(lib, rc, what):
 
 
 @pytest.mark.parametrize("D,H,Hk,M,N,B", [(128, 32, 8, 64, 1000, 2), (64, 8, 8, 10, 20, 1), (128, 32, 8, 5, 4096, 1),
-                                         (64, 16, 4, 33, 777, 1), (128, 8, 2, 16, 300, 1)])
+                                         (64, 16, 4, 33, 777, 1), (128, 8, 2, 16, 300, 1),
+                                         (128, 16, 4, 24, 3000, 1), (128, 16, 4, 24, 20000, 1)])
 def test_prefix_attention(dry, D, H, Hk, M, N, B):
     a = Alloc()
     q, k, v = tensor(a, (B, M, H, D)), tensor(a, (B, N, Hk, D)), tensor(a, (B, N, Hk, D))
@@ -128,7 +129,9 @@ def pool_half(pool, layer, kv):
     # the page sizes of tests/test_gpu_attention.py::test_tree_verify_page_sizes
     (1000, 64, 1, 8, 2, 128, False), (1000, 64, 2, 8, 2, 128, False), (1000, 64, 4, 8, 2, 64, False),
     (1000, 64, 8, 8, 2, 128, False), (1000, 64, 32, 8, 2, 128, True), (1000, 64, 64, 8, 2, 128, False),
-    (5000, 48, 256, 8, 2, 128, False)])
+    (5000, 48, 256, 8, 2, 128, False),
+    # several 256-row blocks per KV head over many splits
+    (6000, 256, 16, 32, 8, 128, False), (30000, 192, 16, 32, 8, 128, False)])
 def test_tree_verify_paged_and_dense(dry, n_prefix, M, ps, H, Hk, D, perm):
     a = Alloc()
     B = 1

@@ -177,7 +177,7 @@ def oracle_tree_verify(inp, heads=None):
     return oa.tree_verify(q, k, v, inp.n_prefix, inp.parent)
 
 
-@pytest.mark.parametrize("n_prefix,M", [(4096, 64), (0, 64), (100, 7), (1000, 128), (16, 256)])
+@pytest.mark.parametrize("n_prefix,M", [(4096, 64), (0, 64), (100, 7), (1000, 128), (16, 256), (6000, 256), (30000, 192)])
 def test_tree_verify_paged_matches_oracle(gpu, n_prefix, M):
     print(f"[tree_verify paged] n_prefix={n_prefix} M={M}", flush=True)
     inp = paged_case(gpu, n_prefix, M, tree_seed=n_prefix + M)
