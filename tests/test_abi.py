@@ -1,6 +1,7 @@
 """The C-ABI library (CPU-side checks only: no kernel is launched here).
 
-  * libdsv.so loads and exports every function include/dsv.h declares;
+  * libdsv.so loads and exports every function include/dsv.h declares, and a C99
+    caller compiles against the header and links every declaration;
   * the ctypes signature table matches the header;
   * argument validation fails loudly with an error code and a message;
   * the Python API refuses CPU tensors (no CPU fallback exists).
@@ -35,6 +36,33 @@ def test_library_exports_every_declared_symbol(dsv_lib):
     for name in declared_functions():
         assert hasattr(dsv_lib, name), f"{name} declared in dsv.h but not exported"
         assert name in _ext.SIGNATURES, f"{name} has no ctypes signature"
+
+
+def test_header_is_plain_c_and_links_every_declaration(dsv_lib, tmp_path):
+    """A C99 caller (gcc -pedantic -Werror) compiles against dsv.h and links every
+    declared function against the built library: the declarations are C, and
+    each names an exported symbol with C linkage."""
+    import shutil
+    import subprocess
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not available")
+    names = declared_functions()
+    src = tmp_path / "caller.c"
+    src.write_text('#include "dsv.h"\n#include <stdio.h>\ntypedef void (*any_fn)(void);\nint main(void) {\n'
+                   '  any_fn fns[] = {\n'
+                   + "".join(f"    (any_fn)&{n},\n" for n in names)
+                   + "  };\n  printf(\"%d %d\\n\", (int)(sizeof(fns) / sizeof(fns[0])), dsv_version());\n"
+                   "  return 0;\n}\n")
+    lib = Path(_ext.lib_path())
+    exe = tmp_path / "caller"
+    cmd = [gcc, "-std=c99", "-Wall", "-Wextra", "-pedantic", "-Werror", f"-I{HEADER.parent}", str(src),
+           f"-L{lib.parent}", f"-l{lib.stem[3:]}", f"-Wl,-rpath,{lib.parent}", "-o", str(exe)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    assert res.returncode == 0, res.stderr
+    run = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+    assert run.returncode == 0, run.stderr
+    assert run.stdout.split() == [str(len(names)), "1"]
 
 
 def test_version(dsv_lib):
