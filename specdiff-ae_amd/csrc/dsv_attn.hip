@@ -222,6 +222,16 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
   }
   if (is_tree) {
     const int M = a.M;
+    // The parent array is staged in the DMA ring, idle until the first tile
+    // is issued after the barrier that ends the set-up: the ancestor walks
+    // then hop through LDS instead of chains of dependent global loads.
+    static_assert(kTreeMaxM * 4 <= G::RING, "parent staging fits the ring");
+    int32_t* par_lds = reinterpret_cast<int32_t*>(smem);
+    if (a.tpar != nullptr) {
+      for (int i = tid; i < M; i += NT)
+        par_lds[i] = (int32_t)load_index(a.tpar, a.tpar_i64, b * a.tpar_sb + i * a.tpar_sm);
+      __syncthreads();
+    }
     for (int i = tid; i < M; i += NT) {
       uint64_t wd[kTreeMaxW];
 #pragma unroll
@@ -232,7 +242,7 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
 #pragma unroll
           for (int x = 0; x < kTreeMaxW; ++x)
             if ((node >> 6) == x) wd[x] |= 1ull << (node & 63);
-          const int p = (int)load_index(a.tpar, a.tpar_i64, b * a.tpar_sb + node * a.tpar_sm);
+          const int p = par_lds[node];
           if (p == node) break;
           node = p;
         }
