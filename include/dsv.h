@@ -67,10 +67,12 @@ const char* dsv_last_error(void);
 /*
  * Instrumentation (no reference counterpart; the reference times phases with
  * host clocks under DIFFSPEC_PROFILE, draft/diffspec_model.py:594-605).
- * Arms a one-shot pair of caller-created hipEvent_t handles: the next entry
- * point called on this thread records `start` on its stream right before its
- * main kernel (kernel 1 for attention, the vocab sweep for acceptance) and
- * `stop` right after it, then disarms.  Pass NULLs to disarm.
+ * Arms a one-shot pair of caller-created hipEvent_t handles for the next
+ * entry point called on this thread, then disarms.  Attention entry points
+ * attach them to kernel 1's own launch (hipExtLaunchKernel): they take that
+ * kernel's start and end times, so their interval is its execution time.
+ * Acceptance entry points record `start` on their stream right before the
+ * vocabulary sweep and `stop` right after it.  Pass NULLs to disarm.
  */
 int dsv_set_timing_events(void* start_event, void* stop_event);
 

@@ -307,10 +307,8 @@ int run(const AttnArgs& a_in, const MergeArgs& m, int dtype, int D, bool dmask, 
   }
   hipEvent_t ev0, ev1;
   take_events(ev0, ev1);
-  if (ev0 != nullptr && hipEventRecord(ev0, st) != hipSuccess) return fail(DSV_ERR_HIP, "hipEventRecord(start) failed");
-  hipError_t e = dsv::launch_attn(a, dtype, D, dmask, st);
+  hipError_t e = dsv::launch_attn(a, dtype, D, dmask, st, ev0, ev1);
   if (e != hipSuccess) return hip_fail(e, "attention kernel launch");
-  if (ev1 != nullptr && hipEventRecord(ev1, st) != hipSuccess) return fail(DSV_ERR_HIP, "hipEventRecord(stop) failed");
   e = dsv::launch_merge(m, st);
   if (e != hipSuccess) return hip_fail(e, "merge kernel launch");
   return DSV_OK;

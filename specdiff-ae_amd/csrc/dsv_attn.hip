@@ -34,6 +34,8 @@
 // O + LSE with an online softmax), :220-292 (tree block), :40-63 (naive tree
 // attention), runtime/bundle_verifier.py:26-135 (masked bundle attention).
 
+#include <hip/hip_ext.h>
+
 #include "dsv_attn_geo.h"
 #include "dsv_dma.h"
 #include "dsv_internal.h"
@@ -645,8 +647,21 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
   if (lg == 0) a.ml[prow] = make_float2(mx, ltot);
 }
 
+// A launch with timing events records them from the kernel's own dispatch
+// packet (its start and end), so their interval is the kernel's execution
+// time; without events it is a plain launch.
+template <typename K>
+hipError_t launch_k(K kernel, dim3 grid, dim3 block, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1,
+                    const AttnArgs& a) {
+  if (ev0 != nullptr || ev1 != nullptr)
+    hipExtLaunchKernelGGL(kernel, grid, block, 0, s, ev0, ev1, 0, a);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, 0, s, a);
+  return hipGetLastError();
+}
+
 template <typename T, int D, bool DMASK>
-hipError_t launch_t(const AttnArgs& a, hipStream_t s) {
+hipError_t launch_t(const AttnArgs& a, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
   const int64_t nblk = (int64_t)a.B * a.Hk * a.s_total * a.n_rb;
   if (nblk <= 0) return hipSuccess;
   // Both sources in 32-bit mode and of one kind: the specialised kernel.
@@ -655,22 +670,18 @@ hipError_t launch_t(const AttnArgs& a, hipStream_t s) {
   const dim3 grid((unsigned)nblk), block(512);
   if constexpr (!DMASK) {
     if (mp == kFast32 && mt == kFast32 && pp == tp) {
-      if (pp)
-        hipLaunchKernelGGL((attn_splitk_kernel<T, D, DMASK, kModeF32Paged>), grid, block, 0, s, a);
-      else
-        hipLaunchKernelGGL((attn_splitk_kernel<T, D, DMASK, kModeF32Dense>), grid, block, 0, s, a);
-      return hipGetLastError();
+      if (pp) return launch_k(attn_splitk_kernel<T, D, DMASK, kModeF32Paged>, grid, block, s, ev0, ev1, a);
+      return launch_k(attn_splitk_kernel<T, D, DMASK, kModeF32Dense>, grid, block, s, ev0, ev1, a);
     }
   }
-  hipLaunchKernelGGL((attn_splitk_kernel<T, D, DMASK, kModeAny>), grid, block, 0, s, a);
-  return hipGetLastError();
+  return launch_k(attn_splitk_kernel<T, D, DMASK, kModeAny>, grid, block, s, ev0, ev1, a);
 }
 
 template <typename T, bool DMASK>
-hipError_t launch_d(const AttnArgs& a, int D, hipStream_t s) {
+hipError_t launch_d(const AttnArgs& a, int D, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1) {
   switch (D) {
-    case 64: return launch_t<T, 64, DMASK>(a, s);
-    case 128: return launch_t<T, 128, DMASK>(a, s);
+    case 64: return launch_t<T, 64, DMASK>(a, s, ev0, ev1);
+    case 128: return launch_t<T, 128, DMASK>(a, s, ev0, ev1);
     default: return hipErrorInvalidValue;
   }
 }
@@ -680,9 +691,10 @@ hipError_t launch_d(const AttnArgs& a, int D, hipStream_t s) {
 int attn_rows_per_block() { return 256; }
 int attn_blocks_per_cu() { return 1; }
 
-hipError_t launch_attn(const AttnArgs& a, int dtype, int D, bool dmask, hipStream_t s) {
-  if (dtype == 0) return dmask ? launch_d<BF16, true>(a, D, s) : launch_d<BF16, false>(a, D, s);
-  return dmask ? launch_d<F16, true>(a, D, s) : launch_d<F16, false>(a, D, s);
+hipError_t launch_attn(const AttnArgs& a, int dtype, int D, bool dmask, hipStream_t s, hipEvent_t ev0,
+                       hipEvent_t ev1) {
+  if (dtype == 0) return dmask ? launch_d<BF16, true>(a, D, s, ev0, ev1) : launch_d<BF16, false>(a, D, s, ev0, ev1);
+  return dmask ? launch_d<F16, true>(a, D, s, ev0, ev1) : launch_d<F16, false>(a, D, s, ev0, ev1);
 }
 
 }  // namespace dsv

@@ -204,7 +204,10 @@ struct LmArgs {
 // ---------------------------------------------------------------------------
 // Launchers (defined in the .hip files, called by the C-ABI layer).
 // ---------------------------------------------------------------------------
-hipError_t launch_attn(const AttnArgs& a, int dtype, int D, bool dmask, hipStream_t s);
+// ev0 / ev1 (may be null): timing events that take the kernel's own start and
+// end times.
+hipError_t launch_attn(const AttnArgs& a, int dtype, int D, bool dmask, hipStream_t s, hipEvent_t ev0 = nullptr,
+                       hipEvent_t ev1 = nullptr);
 // What the host plan needs from the attention kernel's workgroup shape.
 int attn_rows_per_block();
 int attn_blocks_per_cu();
