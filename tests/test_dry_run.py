@@ -131,7 +131,9 @@ def pool_half(pool, layer, kv):
     (1000, 64, 8, 8, 2, 128, False), (1000, 64, 32, 8, 2, 128, True), (1000, 64, 64, 8, 2, 128, False),
     (5000, 48, 256, 8, 2, 128, False),
     # several 256-row blocks per KV head over many splits
-    (6000, 256, 16, 32, 8, 128, False), (30000, 192, 16, 32, 8, 128, False)])
+    (6000, 256, 16, 32, 8, 128, False), (30000, 192, 16, 32, 8, 128, False),
+    # the second workload of tests/test_gpu_graphs.py
+    (1000, 20, 16, 32, 8, 128, False)])
 def test_tree_verify_paged_and_dense(dry, n_prefix, M, ps, H, Hk, D, perm):
     a = Alloc()
     B = 1
