@@ -20,6 +20,7 @@ import torch
 from diffspec_mi355x import workloads as wl
 from diffspec_mi355x.core.bundle_scheduler import bundle_row_order_device
 from diffspec_mi355x.draft.tree_verification import kv_commit, lmhead_tree_accept, tree_accept
+from diffspec_mi355x.runtime.cache_state import append_tree_kv
 from diffspec_mi355x.runtime.tree_attention import tree_verify
 
 pytestmark = pytest.mark.gpu
@@ -156,4 +157,39 @@ def test_kv_commit_graph_replays(gpu):
         torch.cuda.synchronize()
         assert torch.equal(cache, want), f"replay {r}: committed cache differs from the eager result"
         between()
+        torch.cuda.synchronize()
+
+
+def test_kv_append_graph_replays(gpu):
+    print("[graph] kv append + RoPE dense", flush=True)
+    gen = torch.Generator().manual_seed(12)
+    M, Hk, H, D, S, start = 37, 4, 16, 128, 120, 70
+    dt = torch.bfloat16
+    k = (torch.randn((M, Hk, D), generator=gen) * 2).to(dt).to(gpu)
+    v = torch.randn((M, Hk, D), generator=gen).to(dt).to(gpu)
+    q = (torch.randn((1, M, H, D), generator=gen) * 2).to(dt).to(gpu)
+    pos = torch.arange(5000, 5000 + M, dtype=torch.float32)
+    inv = 1.0 / (5e5 ** (torch.arange(0, D, 2, dtype=torch.float32) / D))
+    emb = torch.cat([pos[:, None] * inv[None], pos[:, None] * inv[None]], -1)
+    cos, sin = emb.cos().to(dt).to(gpu), emb.sin().to(dt).to(gpu)
+    k0 = torch.randn((1, Hk, S, D), generator=gen).to(dt).to(gpu)
+    v0 = torch.randn((1, Hk, S, D), generator=gen).to(dt).to(gpu)
+    kc, vc = k0.clone(), v0.clone()
+    q_want = append_tree_kv(k, v, kc, vc, start, cos=cos, sin=sin, q=q).clone()
+    k_want, v_want = kc.clone(), vc.clone()
+    kc.copy_(k0)
+    vc.copy_(v0)
+    torch.cuda.synchronize()
+    g, out = _capture(lambda: append_tree_kv(k, v, kc, vc, start, cos=cos, sin=sin, q=q))
+    ks, vs = k0.clone(), v0.clone()
+    for r in range(3):
+        kc.copy_(k0)
+        vc.copy_(v0)
+        out[0].zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out[0], q_want), f"replay {r}: rotated q differs from the eager result"
+        assert torch.equal(kc, k_want) and torch.equal(vc, v_want), f"replay {r}: cache differs from the eager result"
+        append_tree_kv(k[:5], v[:5], ks, vs, 3)
         torch.cuda.synchronize()
