@@ -117,6 +117,27 @@ int dsv_prefix_attention_forward(const dsv_tensor* q, const dsv_tensor* k,
                                  void* stream);
 
 /*
+ * flash_attn_with_kvcache — runtime/attention_compat.py:103-132 (the
+ * flash-attn contract it stands in for: keys [0, cache_seqlens[b]) of batch
+ * b, causal masking aligned to the end of that range, softmax_lse
+ * [B, H, M]).
+ *   q              [B, M, H, D] bf16|f16;  k_cache, v_cache [B, N, Hk, D]
+ *   cache_seqlens  optional [B] int32|int64 per-batch length (clamped to
+ *                  [0, n_keys]); ndim 0 = every batch uses n_keys
+ *   n_keys         scalar length (the reference's int cache_seqlens); < 0 = N
+ *   causal         != 0: query m of batch b sees keys n <= len_b - M + m
+ *                  (flash-attn's bottom-right alignment for M <= len_b)
+ *   out [B, M, H, D] q dtype or f32;  softmax_lse optional [B, H, M] f32
+ * A query row with no visible key gets out = 0 and lse = -inf.
+ */
+int dsv_flash_attn_with_kvcache(const dsv_tensor* q, const dsv_tensor* k_cache,
+                                const dsv_tensor* v_cache,
+                                const dsv_tensor* cache_seqlens, int64_t n_keys,
+                                int causal, dsv_tensor* out,
+                                dsv_tensor* softmax_lse, void* workspace,
+                                size_t workspace_bytes, void* stream);
+
+/*
  * tree_attention_forward — runtime/tree_attention.py:462-541 (mask handling of
  * _maybe_to_int8_mask, :449-460).
  *   q   [B, M, H, D];  k, v [B, M, Hk, D] (the post-cache tree block)
@@ -180,7 +201,10 @@ int dsv_verify_bundle_paged(const dsv_tensor* q, const dsv_tensor* kv_pages,
  *   parent     [B, M] or [M] int32|int64: parent node of each tree node, < 0 for
  *              the root (the ancestor relation of runtime/draft_tree.py:188-214)
  *   row_perm   optional [M] int32 node order used to pack query rows (bundle
- *              order, core/bundle_scheduler.py:42-123); ndim == 0 = identity
+ *              order, core/bundle_scheduler.py:42-123); ndim == 0 = identity.
+ *              It must be a permutation of [0, M) (dsv_bundle_order's output
+ *              is one): entries are clamped into [0, M), and a repeated
+ *              entry leaves the rows of the missing nodes unwritten.
  *   out [B, M, H, D] bf16|f16|f32;  lse [B, M, H] f32 (ndim == 0 to skip)
  */
 int dsv_tree_verify(const dsv_tensor* q, const dsv_tensor* k,
@@ -307,6 +331,10 @@ int dsv_lmhead_accept(int mode, const dsv_tensor* hidden, const dsv_tensor* weig
  *   start       cache length before the tree (first tree token)
  *   q, q_out    optional [M, H, D] or [1, M, H, D] (ndim 0 to skip)
  * D must be a multiple of 16; token rows 16-byte aligned.
+ * Aliasing: inputs (k, v, q, cos, sin) may not overlap outputs (k_dst, v_dst,
+ * q_out), nor outputs each other (DSV_ERR_INVALID), except row for row in
+ * place: q_out == q with the same strides, or, with a dense cache, k (v)
+ * being exactly k_dst's (v_dst's) tree slots [start, start + M).
  */
 int dsv_kv_append(const dsv_tensor* k, const dsv_tensor* v, const dsv_tensor* cos,
                   const dsv_tensor* sin, dsv_tensor* k_dst, dsv_tensor* v_dst,

@@ -390,9 +390,15 @@ size_t dsv_attn_workspace_bytes(int64_t B, int64_t M, int64_t H, int64_t Hk, int
   return make_plan(B, M, H, Hk, D, n_keys, page_size, has_tree != 0).total;
 }
 
-int dsv_prefix_attention_forward(const dsv_tensor* q, const dsv_tensor* k, const dsv_tensor* v, int64_t n_keys,
-                                 dsv_tensor* out, dsv_tensor* lse, void* workspace, size_t workspace_bytes,
-                                 void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Prefix attention with an optional per-batch length and causal mask: the
+// body of dsv_prefix_attention_forward and dsv_flash_attn_with_kvcache.
+int prefix_attention(const dsv_tensor* q, const dsv_tensor* k, const dsv_tensor* v, const dsv_tensor* seqlens,
+                     int64_t n_keys, int causal, dsv_tensor* out, dsv_tensor* lse, void* workspace,
+                     size_t workspace_bytes, void* stream) {
   int rc;
   if ((rc = check_q_out(q, out)) != DSV_OK) return rc;
   if ((rc = check_kv_dense(k, v, q, "k", "v")) != DSV_OK) return rc;
@@ -400,9 +406,16 @@ int dsv_prefix_attention_forward(const dsv_tensor* q, const dsv_tensor* k, const
   const int64_t N = k->shape[1], Hk = k->shape[2];
   if (n_keys < 0) n_keys = N;
   if (n_keys > N) return fail(DSV_ERR_INVALID, "n_keys (%lld) exceeds the key length (%lld)", (long long)n_keys, (long long)N);
-  if ((rc = check_nd(lse, "lse", 3)) != DSV_OK) return rc;
-  if (lse->dtype != DSV_F32 || lse->shape[0] != B || lse->shape[1] != H || lse->shape[2] != M)
-    return fail(DSV_ERR_INVALID, "lse must be float32 [B, H, M]");
+  if (present(seqlens)) {
+    if ((rc = check_nd(seqlens, "cache_seqlens", 1)) != DSV_OK) return rc;
+    if ((seqlens->dtype != DSV_I32 && seqlens->dtype != DSV_I64) || seqlens->shape[0] != B || seqlens->stride[0] != 1)
+      return fail(DSV_ERR_INVALID, "cache_seqlens must be a contiguous int32|int64 [B] tensor");
+  }
+  if (present(lse)) {
+    if ((rc = check_nd(lse, "lse", 3)) != DSV_OK) return rc;
+    if (lse->dtype != DSV_F32 || lse->shape[0] != B || lse->shape[1] != H || lse->shape[2] != M)
+      return fail(DSV_ERR_INVALID, "lse must be float32 [B, H, M]");
+  }
   const Plan p = make_plan(B, M, H, Hk, D, n_keys, 0, false);
   if ((rc = check_ws(p, workspace, workspace_bytes)) != DSV_OK) return rc;
 
@@ -410,17 +423,42 @@ int dsv_prefix_attention_forward(const dsv_tensor* q, const dsv_tensor* k, const
   fill_common(a, q, Hk, p, workspace);
   a.pre = dense_src(k, v, 0);
   a.n_pre = n_keys;
+  if (present(seqlens)) {
+    a.seqlens = seqlens->data;
+    a.seqlens_i64 = seqlens->dtype == DSV_I64;
+  }
+  a.causal = causal != 0;
   MergeArgs m{};
   fill_merge(m, a, out, (int)D);
-  m.lse = static_cast<float*>(lse->data);
-  m.l_sb = lse->stride[0];
-  m.l_sh = lse->stride[1];
-  m.l_sm = lse->stride[2];
+  if (present(lse)) {
+    m.lse = static_cast<float*>(lse->data);
+    m.l_sb = lse->stride[0];
+    m.l_sh = lse->stride[1];
+    m.l_sm = lse->stride[2];
+  }
   AttnExtents ex = common_extents(q, out, workspace, p);
   ex.pre_k = extent_of("k", k);
   ex.pre_v = extent_of("v", v);
   ex.lse = extent_of("lse", lse);
   return run(a, m, q->dtype, (int)D, false, static_cast<hipStream_t>(stream), ex);
+}
+
+}  // namespace
+
+extern "C" {
+
+int dsv_prefix_attention_forward(const dsv_tensor* q, const dsv_tensor* k, const dsv_tensor* v, int64_t n_keys,
+                                 dsv_tensor* out, dsv_tensor* lse, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+  if (!present(lse)) return fail(DSV_ERR_INVALID, "lse must be float32 [B, H, M]");
+  return prefix_attention(q, k, v, nullptr, n_keys, 0, out, lse, workspace, workspace_bytes, stream);
+}
+
+int dsv_flash_attn_with_kvcache(const dsv_tensor* q, const dsv_tensor* k_cache, const dsv_tensor* v_cache,
+                                const dsv_tensor* cache_seqlens, int64_t n_keys, int causal, dsv_tensor* out,
+                                dsv_tensor* softmax_lse, void* workspace, size_t workspace_bytes, void* stream) {
+  return prefix_attention(q, k_cache, v_cache, cache_seqlens, n_keys, causal, out, softmax_lse, workspace,
+                          workspace_bytes, stream);
 }
 
 int dsv_tree_attention_forward(const dsv_tensor* q, const dsv_tensor* k, const dsv_tensor* v,
@@ -578,9 +616,13 @@ int dsv_verify_bundle_paged(const dsv_tensor* q, const dsv_tensor* kv_pages, con
   return run(a, m, q->dtype, (int)D, true, static_cast<hipStream_t>(stream), ex);
 }
 
-int dsv_tree_verify(const dsv_tensor* q, const dsv_tensor* k, const dsv_tensor* v, const dsv_tensor* page_table,
-                    int64_t n_prefix, const dsv_tensor* parent, const dsv_tensor* row_perm, dsv_tensor* out,
-                    dsv_tensor* lse, void* workspace, size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+int tree_verify_impl(const dsv_tensor* q, const dsv_tensor* k, const dsv_tensor* v, const dsv_tensor* page_table,
+                     int64_t n_prefix, const dsv_tensor* parent, const dsv_tensor* row_perm, dsv_tensor* out,
+                     dsv_tensor* lse, void* workspace, size_t workspace_bytes, void* stream) {
   int rc;
   if ((rc = check_q_out(q, out)) != DSV_OK) return rc;
   const int64_t B = q->shape[0], M = q->shape[1], H = q->shape[2], D = q->shape[3];
@@ -684,6 +726,18 @@ int dsv_tree_verify(const dsv_tensor* q, const dsv_tensor* k, const dsv_tensor* 
   ex.lse = extent_of("lse", lse);
   return run(a, m, q->dtype, (int)D, false, static_cast<hipStream_t>(stream), ex);
 }
+
+}  // namespace
+
+extern "C" {
+
+int dsv_tree_verify(const dsv_tensor* q, const dsv_tensor* k, const dsv_tensor* v, const dsv_tensor* page_table,
+                    int64_t n_prefix, const dsv_tensor* parent, const dsv_tensor* row_perm, dsv_tensor* out,
+                    dsv_tensor* lse, void* workspace, size_t workspace_bytes, void* stream) {
+  return tree_verify_impl(q, k, v, page_table, n_prefix, parent, row_perm, out, lse, workspace, workspace_bytes,
+                          stream);
+}
+
 
 // ----------------------------------------------------------------------------
 // Acceptance
@@ -833,6 +887,53 @@ int dsv_kv_append(const dsv_tensor* k, const dsv_tensor* v, const dsv_tensor* co
       }
     }
     if (start + M > S) return fail(DSV_ERR_INVALID, "tokens [start, start + M) exceed the cache");
+  }
+  // Aliasing: a thread reads one row's chunk pair and writes the same pair of
+  // the destination row, so a row rotated in place is safe; any other overlap
+  // of a read operand with a written one would let one thread overwrite what
+  // another still has to read.  Exact in place: q_out == q, or (dense cache)
+  // k / v already sitting in the destination's tree slots.
+  {
+    struct Span {
+      const char* name;
+      uintptr_t lo, hi;
+    };
+    auto span = [&](const char* nm, const dsv_tensor* t) {
+      const uintptr_t lo = present(t) ? reinterpret_cast<uintptr_t>(t->data) : 0;
+      return Span{nm, lo, present(t) ? lo + (uintptr_t)span_bytes(t) : lo};
+    };
+    auto in_place = [&](const dsv_tensor* src, const dsv_tensor* dst, int64_t dst_st, int64_t dst_sh) {
+      if (!present(src) || !present(dst)) return false;
+      const int o = src->ndim - 3;
+      if (dst == q_out)
+        return src->data == dst->data && src->stride[o] == dst->stride[dst->ndim - 3] &&
+               src->stride[o + 1] == dst->stride[dst->ndim - 2];
+      if (present(page_table)) return false;
+      return reinterpret_cast<uintptr_t>(src->data) == reinterpret_cast<uintptr_t>(dst->data) + (uintptr_t)(start * dst_st * 2) &&
+             src->stride[o] == dst_st && src->stride[o + 1] == dst_sh;
+    };
+    const dsv_tensor* srcs[5] = {k, v, q, cos, sin};
+    const char* snames[5] = {"k", "v", "q", "cos", "sin"};
+    const dsv_tensor* dsts[3] = {k_dst, v_dst, q_out};
+    const char* dnames[3] = {"k_dst", "v_dst", "q_out"};
+    const int64_t dst_st[3] = {a.kd_st, a.vd_st, 0}, dst_sh[3] = {a.kd_sh, a.vd_sh, 0};
+    for (int si = 0; si < 5; ++si) {
+      const Span s = span(snames[si], srcs[si]);
+      if (s.hi == s.lo) continue;
+      for (int di = 0; di < 3; ++di) {
+        const Span d = span(dnames[di], dsts[di]);
+        if (d.hi == d.lo || s.hi <= d.lo || d.hi <= s.lo) continue;
+        if (si == di && in_place(srcs[si], dsts[di], dst_st[di], dst_sh[di])) continue;
+        return fail(DSV_ERR_INVALID, "%s overlaps %s: inputs may not alias an output except row for row in place",
+                    s.name, d.name);
+      }
+    }
+    for (int i = 0; i < 3; ++i)
+      for (int j = i + 1; j < 3; ++j) {
+        const Span x = span(dnames[i], dsts[i]), y = span(dnames[j], dsts[j]);
+        if (x.hi > x.lo && y.hi > y.lo && x.lo < y.hi && y.lo < x.hi)
+          return fail(DSV_ERR_INVALID, "%s overlaps %s: outputs may not alias each other", x.name, y.name);
+      }
   }
   if (g_dry_run) return DSV_OK;
   const hipError_t e = dsv::launch_append(a, static_cast<hipStream_t>(stream));

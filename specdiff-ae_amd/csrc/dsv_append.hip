@@ -12,9 +12,10 @@
 // runtime/cache_state.py:52-66 and the per-token PagedKVCache.write_kv of
 // core/kv_cache/paged_kv.py:168-223 in the reference).
 //
-// One thread per 16-byte chunk (8 elements) of a token row: it loads its
-// chunk and the partner chunk D/2 away (rotate_half), the token's cos/sin
-// chunks, and stores one chunk.
+// One thread per pair of 16-byte chunks (8 elements each) D/2 apart in a
+// token row: it loads both chunks (each is the other's rotate_half partner)
+// and the token's cos/sin chunks before it stores either, so a row rotated
+// in place (q_out == q) never reads a chunk another thread has written.
 
 #include "dsv_internal.h"
 
@@ -41,14 +42,16 @@ __device__ __forceinline__ u32x4 rope8(u32x4 x, u32x4 part, u32x4 c, u32x4 s, bo
   // sum (an FMA through the float widening would skip that rounding).
 #pragma clang fp contract(off)
   u32x4 out;
+  // rotate_half: -x[e + D/2] for e < D/2, x[e - D/2] above; the negation
+  // flips the 16-bit sign bits (exact, like negating the widened value).
+  if (first_half) part ^= u32x4{0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u};
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
     uint32_t o = 0;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const float xv = h2f<F16>((uint16_t)(x[w] >> (16 * h)));
-      float pv = h2f<F16>((uint16_t)(part[w] >> (16 * h)));
-      if (first_half) pv = -pv;  // rotate_half: -x[e + D/2] for e < D/2, x[e - D/2] above
+      const float pv = h2f<F16>((uint16_t)(part[w] >> (16 * h)));
       const float cv = h2f<F16>((uint16_t)(c[w] >> (16 * h))), sv = h2f<F16>((uint16_t)(s[w] >> (16 * h)));
       const float a = h2f<F16>(f2h<F16>(xv * cv));
       const float b = h2f<F16>(f2h<F16>(pv * sv));
@@ -61,16 +64,14 @@ __device__ __forceinline__ u32x4 rope8(u32x4 x, u32x4 part, u32x4 c, u32x4 s, bo
 
 template <bool F16>
 __global__ void __launch_bounds__(256) kv_append_kernel(const AppendArgs a) {
-  const int cpr = a.D / 8;  // chunks per row
+  const int half = a.D / 16;  // chunk pairs per row
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   // Rows: [0, M*Hk) keys, [M*Hk, 2*M*Hk) values, then M*H query rows.
   const int64_t nkv = (int64_t)a.M * a.Hk;
   const int64_t rows = 2 * nkv + (a.q != nullptr ? (int64_t)a.M * a.H : 0);
-  if (idx >= rows * cpr) return;
-  const int64_t row = idx / cpr;
-  const int ch = (int)(idx - row * cpr);
-  const int half = cpr / 2;
-  const int partner = ch < half ? ch + half : ch - half;
+  if (idx >= rows * half) return;
+  const int64_t row = idx / half;
+  const int c0 = (int)(idx - row * half), c1 = c0 + half;
 
   int kind, i, h;  // 0 key, 1 value, 2 query; token i, head h
   if (row < nkv) {
@@ -90,12 +91,17 @@ __global__ void __launch_bounds__(256) kv_append_kernel(const AppendArgs a) {
   const int64_t s_m = kind == 0 ? a.k_sm : (kind == 1 ? a.v_sm : a.q_sm);
   const int64_t s_h = kind == 0 ? a.k_sh : (kind == 1 ? a.v_sh : a.q_sh);
   const uint16_t* xr = src + i * s_m + h * s_h;
-  u32x4 x = *reinterpret_cast<const u32x4*>(xr + ch * 8);
+  u32x4 x0 = *reinterpret_cast<const u32x4*>(xr + c0 * 8);
+  u32x4 x1 = *reinterpret_cast<const u32x4*>(xr + c1 * 8);
   if (kind != 1 && a.cos != nullptr) {
-    const u32x4 part = *reinterpret_cast<const u32x4*>(xr + partner * 8);
-    const u32x4 c = *reinterpret_cast<const u32x4*>(a.cos + i * a.cs_m + ch * 8);
-    const u32x4 s = *reinterpret_cast<const u32x4*>(a.sin + i * a.sn_m + ch * 8);
-    x = rope8<F16>(x, part, c, s, ch < half);
+    const uint16_t* cr = a.cos + i * a.cs_m;
+    const uint16_t* sr = a.sin + i * a.sn_m;
+    const u32x4 cs0 = *reinterpret_cast<const u32x4*>(cr + c0 * 8), cs1 = *reinterpret_cast<const u32x4*>(cr + c1 * 8);
+    const u32x4 sn0 = *reinterpret_cast<const u32x4*>(sr + c0 * 8), sn1 = *reinterpret_cast<const u32x4*>(sr + c1 * 8);
+    const u32x4 y0 = rope8<F16>(x0, x1, cs0, sn0, true);
+    const u32x4 y1 = rope8<F16>(x1, x0, cs1, sn1, false);
+    x0 = y0;
+    x1 = y1;
   }
   uint16_t* dst;
   if (kind == 2) {
@@ -113,14 +119,15 @@ __global__ void __launch_bounds__(256) kv_append_kernel(const AppendArgs a) {
       dst = base + h * (kind == 0 ? a.kd_sh : a.vd_sh) + t * (kind == 0 ? a.kd_st : a.vd_st);
     }
   }
-  *reinterpret_cast<u32x4*>(dst + ch * 8) = x;
+  *reinterpret_cast<u32x4*>(dst + c0 * 8) = x0;
+  *reinterpret_cast<u32x4*>(dst + c1 * 8) = x1;
 }
 
 }  // namespace
 
 hipError_t launch_append(const AppendArgs& a, hipStream_t s) {
   const int64_t rows = 2 * (int64_t)a.M * a.Hk + (a.q != nullptr ? (int64_t)a.M * a.H : 0);
-  const int64_t n = rows * (a.D / 8);
+  const int64_t n = rows * (a.D / 16);
   if (n <= 0) return hipSuccess;
   const dim3 grid((unsigned)((n + 255) / 256)), block(256);
   if (a.f16)

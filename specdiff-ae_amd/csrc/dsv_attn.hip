@@ -200,17 +200,32 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
   const bool is_tree = a.has_tree && split == a.n_splits;
   const KvSrc src = is_tree ? a.tree : a.pre;
 
+  // This batch's prefix length (flash-attn cache_seqlens), clamped to [0, n_pre].
+  int64_t n_pre_b = a.n_pre;
+  if (a.seqlens != nullptr) {
+    n_pre_b = load_index(a.seqlens, a.seqlens_i64, b);
+    n_pre_b = n_pre_b < 0 ? 0 : (n_pre_b > a.n_pre ? a.n_pre : n_pre_b);
+  }
   int64_t kstart, kend;
   if (is_tree) {
     kstart = 0;
     kend = a.M;
   } else {
     kstart = (int64_t)split * a.kps;
-    kend = min(kstart + a.kps, a.n_pre);
+    kend = min(kstart + a.kps, n_pre_b);
   }
   const int64_t nkeys = kend - kstart;
   const int ntiles = nkeys > 0 ? (int)((nkeys + KT - 1) / KT) : 0;
   const int nfull = nkeys > 0 ? (int)(nkeys / KT) : 0;  // tiles without tail keys
+  // Causal prefix (bottom-right aligned): row m sees keys n <= c0 + m with
+  // c0 = len - M.  Tiles below nvis are visible to every row.
+  const bool causal = a.causal != 0 && !is_tree;
+  const int64_t c0 = n_pre_b - a.M;
+  int nvis = nfull;
+  if (causal) {
+    const int64_t v = c0 + 1 - kstart;
+    nvis = v <= 0 ? 0 : (int)min((int64_t)nfull, v / KT);
+  }
   const bool paged = MODE == kModeF32Paged || (MODE == kModeAny && src.pt != nullptr);
   const int mode = MODE == kModeAny ? dma_mode<D>(src) : (int)kFast32;
 
@@ -440,7 +455,8 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
   // Bit v of a lane <-> key 4*lg + 8*(v/4) + v%4 of the tile.
   auto mask_scores = [&](f32x16& s, int t) {
     const int64_t kb = kstart + (int64_t)t * KT;
-    const int lim = (int)min(kend - kb, (int64_t)KT) - 4 * lg;  // valid keys from 4*lg
+    const int64_t ke = causal ? min(kend, c0 + 1 + node_of) : kend;  // this row's key end
+    const int lim = (int)max(min(ke - kb, (int64_t)KT), (int64_t)-KT) - 4 * lg;  // valid keys from 4*lg
     uint32_t keep = 0;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -532,7 +548,7 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
       read_k(IC<(S + 1) & 3>{}, kf);
 
       // ---- Y_k: online softmax of S(k) (log2 domain, lazy rescale) ----------
-      if (is_tree || DMASK || k >= nfull) mask_scores(s_cur, k);
+      if (is_tree || DMASK || k >= nvis) mask_scores(s_cur, k);
       const float mt = xor32_max(max16(s_cur)) * scale_log2;
       if (__ballot(mt > mx + kRescaleTau) != 0ull) {
         const float mn = __builtin_elementwise_maximum(mx, mt);

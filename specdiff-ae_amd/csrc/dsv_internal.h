@@ -23,7 +23,6 @@ struct BF16 {};
 struct F16 {};
 
 // Limits of the in-kernel tables (checked by the host before launch).
-constexpr int kTileKeys = 64;        // keys per LDS tile
 constexpr int kPageLds = 1040;       // page-table entries staged per split
 constexpr int kTreeMaxM = 256;       // tree nodes handled by the tree split
 constexpr int kTreeMaxW = kTreeMaxM / 64;
@@ -58,8 +57,11 @@ struct AttnArgs {
 
   KvSrc pre;               // prefix source
   int64_t n_pre;           // prefix keys [0, n_pre)
+  const void* seqlens;     // optional [B] per-batch prefix length (clamped to [0, n_pre])
+  int seqlens_i64;
+  int causal;              // row m sees prefix keys n <= len_b - M + m (flash-attn causal)
   int n_splits;            // prefix splits
-  int64_t kps;             // prefix keys per split (multiple of kTileKeys)
+  int64_t kps;             // prefix keys per split (whole 32-key tiles, Geo<D>::KT)
 
   // Optional byte mask [Bm, M, N] over the prefix keys (1 = keep).
   const uint8_t* dmask;

@@ -59,6 +59,7 @@ SIGNATURES = {
     "dsv_dry_run_checks": (_I64, []),
     "dsv_attn_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_int]),
     "dsv_prefix_attention_forward": (ctypes.c_int, [_P, _P, _P, _I64, _P, _P, _V, _SZ, _V]),
+    "dsv_flash_attn_with_kvcache": (ctypes.c_int, [_P, _P, _P, _P, _I64, ctypes.c_int, _P, _P, _V, _SZ, _V]),
     "dsv_tree_attention_forward": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _V, _SZ, _V]),
     "dsv_verify_bundle": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _V, _SZ, _V]),
     "dsv_verify_bundle_paged": (ctypes.c_int, [_P, _P, _P, _I64, _P, _P, _P, _V, _SZ, _V]),

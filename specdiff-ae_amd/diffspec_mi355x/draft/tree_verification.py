@@ -155,12 +155,18 @@ def kv_commit(kv: torch.Tensor, start: int, path: torch.Tensor, info: torch.Tens
     _ext.check(rc, "kv_commit")
 
 
-def _kv_commit_ok(t: torch.Tensor) -> bool:
-    """Whether the commit kernel takes this dense cache tensor as it is."""
+# Bytes of tree rows the commit kernel stages per cache row (dsv_kv_commit:
+# M * row bytes <= 256 threads x 16 chunks x 16 bytes).
+KV_COMMIT_MAX_TREE_BYTES = 256 * 16 * 16
+
+
+def _kv_commit_ok(t: torch.Tensor, M: int) -> bool:
+    """Whether the commit kernel takes this dense cache tensor as it is, for an M-node tree."""
     es = t.element_size()
     return (t.is_cuda and t.dtype in (torch.bfloat16, torch.float16, torch.float32) and 3 <= t.dim() <= 6
             and t.stride(-1) == 1 and (t.shape[-1] * es) % 16 == 0 and t.data_ptr() % 16 == 0
-            and all((st * es) % 16 == 0 for st in t.stride()[:-1]))
+            and all((st * es) % 16 == 0 for st in t.stride()[:-1])
+            and M * t.shape[-1] * es <= KV_COMMIT_MAX_TREE_BYTES)
 
 
 def _evaluate_tree_dev(logits, draft, parent, position_ids, max_depth, mode, temperature, posterior_threshold,
@@ -268,7 +274,8 @@ def verify_new(input_ids, logits, draft, position_ids, hidden_states, tree_atten
     # Cache tensors the commit kernel takes are compacted on the GPU from the
     # walk's device-side path; other layouts take the reference's gather + copy.
     for data in past_key_values_data:
-        if _kv_commit_ok(data) and start + int(draft.size(1)) <= data.shape[-2] and data.device == acc["path"].device:
+        if (_kv_commit_ok(data, int(draft.size(1))) and start + int(draft.size(1)) <= data.shape[-2]
+                and data.device == acc["path"].device):
             kv_commit(data, start, acc["path"], acc["info"])
         else:
             tgt = data[..., select_indices.to(data.device), :]

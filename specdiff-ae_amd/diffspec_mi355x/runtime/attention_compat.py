@@ -3,18 +3,20 @@
 Mirrors the contract of the reference's ``diffspec/runtime/attention_compat.py``
 (:103-132): ``flash_attn_with_kvcache(q, k_cache, v_cache, causal,
 cache_seqlens, return_softmax_lse)`` returns ``out [B, M, H, D]`` and, when
-asked, ``lse [B, H, M]`` in float32.  Only the non-causal form used by the
-verification path (llama_target_model.py:838-845) is implemented; causal=True
-raises.
+asked, ``lse [B, H, M]`` in float32.  ``cache_seqlens`` is an int or a
+per-batch tensor (flash-attn's form; the reference's fallback takes only a
+scalar), and ``causal=True`` aligns the mask to the end of each batch's keys
+(query m sees keys n <= len - M + m), as flash-attn does.
+
 """
 
 from __future__ import annotations
 
-from typing import Optional
+from typing import Optional, Union
 
 import torch
 
-from .tree_attention import prefix_attention_forward
+from .. import _ext
 
 # The verification path never imports the flash-attn package; these flags keep
 # callers that branch on them on the HIP path.
@@ -28,26 +30,38 @@ def sdpa_backend_name() -> str:
 
 def flash_attn_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, dropout_p: float = 0.0,
                     causal: bool = False, window_size=None, **_: object) -> torch.Tensor:
-    if causal:
-        raise NotImplementedError("causal attention is not part of the tree-verification kernels")
     if dropout_p:
         raise NotImplementedError("dropout is not supported")
-    B, M, H, D = q.shape
-    out, _ = prefix_attention_forward(q, k, v, B, M, H, D)
-    return out
+    return flash_attn_with_kvcache(q, k, v, causal=causal)
 
 
 def flash_attn_with_kvcache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, causal: bool = False,
-                            cache_seqlens: Optional[int] = None, return_softmax_lse: bool = False, **_: object):
-    if causal:
-        raise NotImplementedError("causal attention is not part of the tree-verification kernels")
-    if isinstance(cache_seqlens, torch.Tensor):
-        if cache_seqlens.numel() != 1:
-            raise NotImplementedError("per-batch cache_seqlens are not supported")
-        cache_seqlens = int(cache_seqlens.item())
+                            cache_seqlens: Optional[Union[int, torch.Tensor]] = None, return_softmax_lse: bool = False,
+                            **_: object):
+    dev = _ext.require_gpu(q, k_cache, v_cache)
     B, M, H, D = q.shape
-    n = -1 if cache_seqlens is None else int(cache_seqlens)
-    out, lse = prefix_attention_forward(q, k_cache, v_cache, B, M, H, D, n_keys=n)
+    N, Hk = k_cache.shape[1], k_cache.shape[2]
+    seqlens, n = None, N
+    if isinstance(cache_seqlens, torch.Tensor):
+        if cache_seqlens.numel() == 1 and cache_seqlens.dim() == 0:
+            n = min(int(cache_seqlens.item()), N)
+        else:
+            seqlens = cache_seqlens.reshape(-1)
+            if seqlens.numel() != B:
+                raise ValueError(f"cache_seqlens must hold one length per batch ({B}), got {seqlens.numel()}")
+            if seqlens.dtype not in (torch.int32, torch.int64):
+                seqlens = seqlens.to(torch.int64)
+            seqlens = seqlens.to(dev).contiguous()
+    elif cache_seqlens is not None:
+        n = int(cache_seqlens)
+    lib = _ext.load()
+    out = torch.empty_like(q)
+    lse = torch.empty((B, H, M), dtype=torch.float32, device=dev) if return_softmax_lse else None
+    ws = _ext.workspace(lib.dsv_attn_workspace_bytes(B, M, H, Hk, D, n, 0, 0), dev)
+    rc = lib.dsv_flash_attn_with_kvcache(_ext.desc(q), _ext.desc(k_cache), _ext.desc(v_cache), _ext.desc(seqlens),
+                                         int(n), int(bool(causal)), _ext.desc(out), _ext.desc(lse), ws.data_ptr(),
+                                         ws.numel(), _ext.stream_of(dev))
+    _ext.check(rc, "flash_attn_with_kvcache")
     if return_softmax_lse:
         return out, lse
     return out

@@ -119,8 +119,18 @@ def tree_attention_forward(query_states, key_states, value_states, tree_mask, ca
     return current_out, weight
 
 
+def _check_row_perm(row_perm: torch.Tensor, M: int) -> None:
+    """A caller-supplied query packing order must be a permutation of [0, M)."""
+    if row_perm.dim() != 1 or row_perm.numel() != M:
+        raise ValueError(f"row_perm must be a [M] = [{M}] permutation (got shape {tuple(row_perm.shape)})")
+    ok = torch.equal(torch.sort(row_perm.to(torch.int64)).values,
+                     torch.arange(M, device=row_perm.device, dtype=torch.int64))
+    if not ok:
+        raise ValueError("row_perm is not a permutation of [0, M): rows of the missing nodes would stay unwritten")
+
+
 def tree_verify(query_states, k_cache, v_cache, n_prefix: int, parent, page_table=None, row_perm=None,
-                out_dtype=None, return_lse: bool = True):
+                out_dtype=None, return_lse: bool = True, check_row_perm: bool = True):
     """Fused hybrid tree verification: prefix + tree block + LSE merge.
 
     Computes what llama_target_model.py:834-867 computes with three calls and
@@ -134,7 +144,11 @@ def tree_verify(query_states, k_cache, v_cache, n_prefix: int, parent, page_tabl
             [n_pages] or [B, n_pages], or contiguous caches [B, L, Hk, D].
             The tree's K/V rows are tokens [n_prefix, n_prefix + M).
         parent: [M] or [B, M] int32/int64, parent node of each node (< 0 = root).
-        row_perm: optional int32 [M] query packing order (bundle order).
+        row_perm: optional int32 [M] query packing order (bundle order), a
+            permutation of [0, M).
+        check_row_perm: verify that ``row_perm`` is a permutation (one device
+            sort and a host read); pass False for an order that is one by
+            construction, such as ``bundle_row_order_device``'s output.
 
     Returns:
         out [B, M, H, D] (out_dtype, default the query dtype) and lse [B, M, H] float32.
@@ -150,8 +164,11 @@ def tree_verify(query_states, k_cache, v_cache, n_prefix: int, parent, page_tabl
         Hk, ps = k_cache.shape[2], 0
     ws_bytes = lib.dsv_attn_workspace_bytes(B, M, H, Hk, D, int(n_prefix), ps, 1)
     ws = _ext.workspace(ws_bytes, dev)
-    if row_perm is not None and row_perm.dtype != torch.int32:
-        row_perm = row_perm.to(torch.int32)
+    if row_perm is not None:
+        if check_row_perm:
+            _check_row_perm(row_perm, M)
+        if row_perm.dtype != torch.int32:
+            row_perm = row_perm.to(torch.int32)
     args = [_ext.desc(query_states), _ext.desc(k_cache), _ext.desc(v_cache), _ext.desc(page_table)]
     rc = lib.dsv_tree_verify(*args, int(n_prefix), _ext.desc(parent), _ext.desc(row_perm), _ext.desc(out),
                              _ext.desc(lse), ws.data_ptr(), ws.numel(), _ext.stream_of(dev))

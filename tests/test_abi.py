@@ -187,14 +187,55 @@ def test_kv_append_validation(dsv_lib):
                                ctypes.byref(dst), ctypes.byref(dst), ctypes.byref(none), 0, ctypes.byref(none),
                                ctypes.byref(none), None)
     assert rc == -1 and "together" in _ext.last_error()
+    dst = _t((2, 40, 64), ptr=0x100000)
+    vdst = _t((2, 40, 64), ptr=0x200000)
     dsv_lib.dsv_set_dry_run(1)
     try:
         rc = dsv_lib.dsv_kv_append(ctypes.byref(k), ctypes.byref(k), ctypes.byref(cos), ctypes.byref(cos),
-                                   ctypes.byref(dst), ctypes.byref(dst), ctypes.byref(none), 32, ctypes.byref(none),
+                                   ctypes.byref(dst), ctypes.byref(vdst), ctypes.byref(none), 32, ctypes.byref(none),
                                    ctypes.byref(none), None)
     finally:
         dsv_lib.dsv_set_dry_run(0)
     assert rc == 0
+
+
+def test_kv_append_rejects_aliasing_except_row_for_row_in_place(dsv_lib):
+    # A thread reads a chunk pair of one row and writes the same pair of the
+    # destination row: exact in-place rotation is safe, any other overlap of
+    # an input with an output is refused before launch.
+    none = _ext.DsvTensor()
+    M, Hk, H, D, S = 8, 2, 4, 64, 40
+    k = _t((M, Hk, D), ptr=0x10000)
+    v = _t((M, Hk, D), ptr=0x20000)
+    cos = _t((M, D), ptr=0x30000)
+    sin = _t((M, D), ptr=0x40000)
+    kd = _t((Hk, S, D), ptr=0x50000)
+    vd = _t((Hk, S, D), ptr=0x60000)
+    q = _t((M, H, D), ptr=0x70000)
+
+    def call(k_, v_, q_, qo_, start=16):
+        dsv_lib.dsv_set_dry_run(1)
+        try:
+            return dsv_lib.dsv_kv_append(ctypes.byref(k_), ctypes.byref(v_), ctypes.byref(cos), ctypes.byref(sin),
+                                         ctypes.byref(kd), ctypes.byref(vd), ctypes.byref(none), start,
+                                         ctypes.byref(q_), ctypes.byref(qo_), None)
+        finally:
+            dsv_lib.dsv_set_dry_run(0)
+
+    assert call(k, v, q, _t((M, H, D), ptr=0x80000)) == 0
+    assert call(k, v, q, q) == 0                                  # q rotated in place
+    shifted = _t((M, H, D), ptr=0x70000 + 2 * D)                  # q_out one head over q
+    assert call(k, v, q, shifted) == -1 and "q overlaps q_out" in _ext.last_error()
+    assert call(k, v, q, _t((M, H, D), ptr=0x50000)) == -1 and "k_dst overlaps q_out" in _ext.last_error()
+    # k already in k_dst's tree slots (token stride D, head stride S * D), row for row
+    start = 16
+    k_in = _ext.DsvTensor()
+    k_in.data, k_in.dtype, k_in.ndim = 0x50000 + start * D * 2, _ext.DSV_BF16, 3
+    for i, (n, st) in enumerate([(M, D), (Hk, S * D), (D, 1)]):
+        k_in.shape[i], k_in.stride[i] = n, st
+    assert call(k_in, v, q, _t((M, H, D), ptr=0x80000), start=start) == 0
+    assert call(k_in, v, q, _t((M, H, D), ptr=0x80000), start=start + 1) == -1   # off by one token
+    assert call(v, v, q, _t((M, H, D), ptr=0x80000)) == 0                        # k and v may share
 
 
 def test_bundle_order_validation(dsv_lib):

@@ -45,6 +45,32 @@ def test_accept_8x64_vocab128256_bit_exact(gpu, mode):
     assert all(info[t, 1] >= a.planted_len[t] for t in range(8))
 
 
+@pytest.mark.parametrize("mode", ["greedy", "typical"])
+def test_accept_fp32_64_nodes_vocab128256_seed1(gpu, mode):
+    """The CPU reference workload's walk at its own size: fp32 logits
+    [1, 64, 128256] N(0, 3) from seed 1, draft ids uniform over the vocab from
+    the same generator (nothing planted), the 64-node tree of seed 0 (depth
+    <= 8, out-degree <= 4)."""
+    M, V = 64, 128256
+    g = torch.Generator().manual_seed(1)
+    logits = torch.randn((1, M, V), generator=g) * 3.0
+    draft = torch.randint(0, V, (1, M), generator=g)
+    parent, depth = wl.make_tree(M, seed=0)
+    pref = torch.tensor([wl.parent_to_reference(parent)], dtype=torch.int64)
+    pos = torch.tensor([4096 + d for d in depth], dtype=torch.int64)
+    kw = dict(temperature=1.0, posterior_threshold=0.09, posterior_alpha=0.3) if mode == "typical" else {}
+    run_and_compare(logits.to(gpu), draft.to(gpu), pref.to(gpu), pos.to(gpu), 8, mode=mode, **kw)
+    # and with the root's argmax planted along the chain to a deep node, so the walk has a path to follow
+    lg = logits[0].numpy()
+    node = int(np.argmax(depth))
+    while node > 0:
+        draft[0, node] = int(np.argmax(lg[parent[node]]))
+        node = parent[node]
+    info = run_and_compare(logits.to(gpu), draft.to(gpu), pref.to(gpu), pos.to(gpu), 8, mode=mode, **kw)
+    if mode == "greedy":
+        assert info[0, 1] == max(depth)
+
+
 def test_typical_accepts_runner_up_that_greedy_rejects(gpu):
     V, M = 5000, 6
     lg = torch.full((1, M, V), -4.0)
@@ -220,3 +246,26 @@ def test_packed_key_sweep_strided_rows_with_short_tail(gpu):
     run_and_compare(lg, a.draft, a.parent_ref, a.pos, 8)
     run_and_compare(lg, a.draft, a.parent_ref, a.pos, 8, mode="typical", temperature=1.0,
                     posterior_threshold=0.09, posterior_alpha=0.3)
+
+
+def test_verify_new_takes_the_reference_copy_beyond_the_commit_kernel_limit(gpu):
+    """A 300-node tree with 128-element fp32 cache rows (300 x 512 B above the
+    commit kernel's 64 KiB of staged tree rows) takes the reference's gather +
+    copy instead of raising."""
+    M = 300
+    a = wl.make_accept_inputs(T=1, M=M, V=3000, device=str(gpu), seed=3, max_outdeg=6, pos_offset=50)
+    L = M + 40
+    kv = [torch.randn(2, 1, 2, L, 128, device=gpu) for _ in range(2)]
+    kv_before = [x.clone() for x in kv]
+    cur_len = torch.tensor([L], dtype=torch.long)
+    start = L - M
+    model = _FakeModel(gpu)
+    res = verify_new(torch.arange(10, device=gpu).unsqueeze(0), a.logits, a.draft, a.pos,
+                     torch.randn(1, M, 4, device=gpu), None, kv, cur_len, a.parent_ref[0], model, nodes=3,
+                     threshold=0.1, max_depth=8, logits_processor=None)
+    w = oacc.greedy_walk(a.logits[0].float().cpu().numpy(), a.draft[0].cpu().numpy(), a.parent_ref[0].tolist(),
+                         a.pos[0].cpu().numpy(), 8)
+    assert res[1] == w[0] and res[2] == w[2]
+    sel = torch.tensor(w[1], device=gpu) + start
+    for x, x0 in zip(kv, kv_before):
+        assert torch.equal(x[..., start:start + len(w[1]), :], x0[..., sel, :])

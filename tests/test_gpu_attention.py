@@ -86,6 +86,38 @@ def test_prefix_attention_expanded_kv_and_cache_seqlens(gpu):
     assert_lse_close(np64(l3[0]), l_ref)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("seqlen_dtype", [torch.int32, torch.int64])
+def test_flash_attn_with_kvcache_per_batch_seqlens(gpu, causal, seqlen_dtype):
+    """flash-attn's contract (runtime/attention_compat.py:103-132 stands in for
+    it): per-batch cache_seqlens, and causal masking aligned to the end of each
+    batch's keys; a row with no visible key has out 0 and lse -inf."""
+    from diffspec_mi355x.runtime.attention_compat import flash_attn_with_kvcache
+    B, M, H, Hk, D, N = 4, 16, 8, 2, 128, 700
+    print(f"[flash_attn_with_kvcache] causal={causal} seqlens={seqlen_dtype}", flush=True)
+    q = rand((B, M, H, D), 41, torch.bfloat16, gpu)
+    k, v = rand((B, N, Hk, D), 42, torch.bfloat16, gpu), rand((B, N, Hk, D), 43, torch.bfloat16, gpu)
+    lens = [700, 123, 9, 0]
+    out, lse = flash_attn_with_kvcache(q, k, v, causal=causal, cache_seqlens=torch.tensor(lens, dtype=seqlen_dtype,
+                                                                                          device=gpu),
+                                       return_softmax_lse=True)
+    torch.cuda.synchronize()
+    assert out.shape == q.shape and lse.shape == (B, H, M)
+    for b, n in enumerate(lens):
+        keep = np.ones((M, N), dtype=bool)
+        keep[:, n:] = False
+        if causal:
+            keep &= np.arange(N)[None, :] <= (n - M + np.arange(M))[:, None]
+        o_ref, l_ref = oa.masked_attention(np64(q[b]), np64(k[b]), np64(v[b]), keep)
+        assert_attn_close(np64(out[b]), o_ref, what=f"b={b}")
+        assert_lse_close(np64(lse[b]).T, l_ref, what=f"b={b}")
+    # a scalar length is the reference's own form
+    o1 = flash_attn_with_kvcache(q, k, v, causal=causal, cache_seqlens=321)
+    o2 = flash_attn_with_kvcache(q, k, v, causal=causal, cache_seqlens=torch.full((B,), 321, device=gpu))
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)
+
+
 def rising_scores_case(profile, B, M, H, Hk, D, N, seed=11):
     """q, k whose scores grow along the key sequence (in nats, after the 1/sqrt(D) scale).
 
@@ -328,38 +360,78 @@ def test_fp32_inputs_4k_ctx_within_tolerance(gpu):
     assert_lse_close(np64(lse[0]), l_ref, tol=5e-2)
 
 
-def test_64k_ctx_64_nodes_subset_heads(gpu):
-    """64K paged prefix, 64-node tree, bf16 N(0,1)*0.5; heads of KV heads 0-1 vs oracle."""
+def test_64k_ctx_64_nodes_all_heads(gpu):
+    """64K paged prefix, 64-node tree, bf16 N(0,1)*0.5: all 32 query heads
+    (every KV head's workgroups) against the fp64 oracle."""
+    print("[64k all heads] tree_verify", flush=True)
     inp = paged_case(gpu, 65536, 64)
     par = torch.tensor(inp.parent, dtype=torch.int64, device=gpu)
     out, lse = tree_verify(inp.q, inp.kv_pages[0, 0], inp.kv_pages[0, 1], 65536, par, page_table=inp.page_table,
                            out_dtype=torch.float32)
     torch.cuda.synchronize()
-    heads = list(range(8))
-    o_ref, l_ref = oracle_tree_verify(inp, heads)
-    assert_attn_close(np64(out[0, :, :8]), o_ref, rel=4e-3)
-    assert_lse_close(np64(lse[0, :, :8]), l_ref)
+    o_ref, l_ref = oracle_tree_verify(inp)
+    for kvh in range(8):
+        hs = slice(4 * kvh, 4 * kvh + 4)
+        assert_attn_close(np64(out[0, :, hs]), o_ref[:, hs], rel=4e-3, what=f"kv head {kvh}")
+        assert_lse_close(np64(lse[0, :, hs]), l_ref[:, hs], what=f"kv head {kvh}")
     # the tree block alone (where the mask matters) on the same data
     out_t, lse_t = tree_verify(inp.q, inp.kv_pages[0, 0], inp.kv_pages[0, 1], 0, par,
                                page_table=inp.page_table[4096:], out_dtype=torch.float32)
     torch.cuda.synchronize()
-    q = np64(inp.q[0])[:, heads]
-    kt = np64(inp.logical_kv(0, 0)[0, 65536:])[:, :2]
-    vt = np64(inp.logical_kv(0, 1)[0, 65536:])[:, :2]
-    o_t, l_t = oa.masked_attention(q, kt, vt, oa.ancestor_mask(inp.parent))
-    assert_attn_close(np64(out_t[0, :, :8]), o_t, rel=4e-3)
-    assert_lse_close(np64(lse_t[0, :, :8]), l_t)
+    kt = np64(inp.logical_kv(0, 0)[0, 65536:])
+    vt = np64(inp.logical_kv(0, 1)[0, 65536:])
+    o_t, l_t = oa.masked_attention(np64(inp.q[0]), kt, vt, oa.ancestor_mask(inp.parent))
+    assert_attn_close(np64(out_t[0]), o_t, rel=4e-3)
+    assert_lse_close(np64(lse_t[0]), l_t)
 
 
-def test_128k_ctx_128_nodes_bundle_packed_subset_heads(gpu):
-    """128K paged prefix, 128-node tree (depth <= 12, out-degree <= 6),
-    query rows packed in bundle order (8 bundles); KV head 0 vs oracle."""
+def test_128k_ctx_128_nodes_bundle_packed_all_heads(gpu):
+    """128K paged prefix, 128-node tree (depth <= 12, out-degree <= 6), query
+    rows packed in bundle order (8 bundles): all 32 query heads (both 256-row
+    blocks of every KV head) against the fp64 oracle."""
+    print("[128k all heads] tree_verify", flush=True)
     inp = paged_case(gpu, 131072, 128, seed=2, tree_seed=2, max_depth=12, max_outdeg=6)
     par = torch.tensor(inp.parent, dtype=torch.int64, device=gpu)
     perm = torch.tensor(bundle_row_order(inp.parent, num_bundles=8), dtype=torch.int32, device=gpu)
     out, lse = tree_verify(inp.q, inp.kv_pages[0, 0], inp.kv_pages[0, 1], 131072, par, page_table=inp.page_table,
                            row_perm=perm, out_dtype=torch.float32)
     torch.cuda.synchronize()
-    o_ref, l_ref = oracle_tree_verify(inp, list(range(4)))
-    assert_attn_close(np64(out[0, :, :4]), o_ref, rel=4e-3)
-    assert_lse_close(np64(lse[0, :, :4]), l_ref)
+    o_ref, l_ref = oracle_tree_verify(inp)
+    for kvh in range(8):
+        hs = slice(4 * kvh, 4 * kvh + 4)
+        assert_attn_close(np64(out[0, :, hs]), o_ref[:, hs], rel=4e-3, what=f"kv head {kvh}")
+        assert_lse_close(np64(lse[0, :, hs]), l_ref[:, hs], what=f"kv head {kvh}")
+
+
+def test_verify_bundle_attention_profile_shape(gpu):
+    """The reference attention microbenchmark's shape (benchmarks/attention_kernel_profile.py:155-161:
+    q_len 48, prefix 32000, 32 heads, head_dim 128, fp16; K/V in the repeat_kv'd
+    form with 32 heads), bundle mask = prefix plus a causal block over the last
+    48 keys, against the fp64 oracle."""
+    B, M, H, D, N = 1, 48, 32, 128, 32000
+    print("[verify_bundle 48 x 32000]", flush=True)
+    q = rand((B, M, H, D), 21, torch.float16, gpu)
+    k = rand((B, N, H, D), 22, torch.float16, gpu)
+    v = rand((B, N, H, D), 23, torch.float16, gpu)
+    mask = torch.ones(M, N, dtype=torch.int8)
+    mask[:, N - M:] = torch.tril(torch.ones(M, M, dtype=torch.int8))
+    mask = mask.to(gpu)
+    ver = FusedBundleVerifier(bundle_size=3, enable_triton=True, device="cuda")
+    o, lse = ver.verify_bundle(q, k, v, [mask], shared_prefix_len=N - M)
+    torch.cuda.synchronize()
+    assert o.dtype == torch.float16 and lse.shape == (B, M, H)
+    o_ref, l_ref = oa.masked_attention(np64(q[0]), np64(k[0]), np64(v[0]), mask.cpu().numpy() != 0)
+    assert_attn_close(np64(o[0]), o_ref)
+    assert_lse_close(np64(lse[0]), l_ref)
+
+
+def test_tree_verify_rejects_a_row_perm_that_is_not_a_permutation(gpu):
+    inp = paged_case(gpu, 100, 16)
+    par = torch.tensor(inp.parent, dtype=torch.int64, device=gpu)
+    bad = torch.arange(16, dtype=torch.int32, device=gpu)
+    bad[3] = 5
+    with pytest.raises(ValueError, match="not a permutation"):
+        tree_verify(inp.q, inp.kv_pages[0, 0], inp.kv_pages[0, 1], 100, par, page_table=inp.page_table, row_perm=bad)
+    with pytest.raises(ValueError, match="permutation"):
+        tree_verify(inp.q, inp.kv_pages[0, 0], inp.kv_pages[0, 1], 100, par, page_table=inp.page_table,
+                    row_perm=bad[:15])
