@@ -176,7 +176,7 @@ def bench_bundle_packed_128k(args, lib, ev):
         if arm is not None:
             lib.dsv_set_timing_events(arm[0], arm[1])
         k, v = pools[i % layers]
-        return tree_verify(inp.q, k, v, N, par, page_table=inp.page_table, row_perm=perm)
+        return tree_verify(inp.q, k, v, N, par, page_table=inp.page_table, row_perm=perm, check_row_perm=False)
 
     n = 20
     for i in range(10):
@@ -252,98 +252,59 @@ def device_us(fn, calls=10, reps=20):
 def bench_llama8b_step(args, lib, ev):
     """One verify step of a Llama-3.1-8B-shaped target (32 layers, hidden 4096,
     32/8 heads, FFN 14336, vocab 128256, RoPE theta 5e5) over a 64-node tree
-    with a 65536-token paged prefix per layer, random N(0, 0.02) bf16 weights.
-    Per layer: RMSNorm, QKV projection, RoPE of q and k at the nodes'
-    positions with the tree K/V written into the pages after the prefix (one
-    dsv_kv_append launch), the fused tree verify (kernels 1 and 3), o_proj,
-    RMSNorm, SwiGLU MLP; then the final norm, lm_head and the acceptance walk
-    (kernel 4).  Projections, norms and the MLP are torch (hipBLASLt) ops:
-    measurement scaffolding around the hot path, not part of it."""
+    with a 65536-token paged prefix per layer, random N(0, 0.02) bf16 weights
+    (workloads.LlamaVerifyStep).  The draft is planted along the root path of
+    a deepest node from the target's own argmax, so the walk accepts that
+    path.  Per layer: RMSNorm, QKV projection, RoPE + tree K/V into the pages
+    (dsv_kv_append), the fused tree verify (kernels 1 and 3), o_proj, RMSNorm,
+    SwiGLU MLP; then the final norm and the lm_head fused with the greedy walk
+    (kernel 5 + kernel 4's walk).  Projections, norms and the MLP are torch
+    (hipBLASLt) ops: measurement scaffolding around the hot path."""
     from diffspec_mi355x import workloads as wl
-    from diffspec_mi355x.draft.tree_verification import lmhead_tree_accept, tree_accept
     from diffspec_mi355x.runtime.cache_state import append_tree_kv
     from diffspec_mi355x.runtime.tree_attention import tree_verify
 
-    L, hid, H, Hk, D, F, V, N, M = 32, 4096, 32, 8, 128, 14336, 128256, 65536, 64
-    dev = "cuda"
-    inp = wl.make_tree_verify_inputs(n_prefix=N, M=M, H=H, Hk=Hk, D=D, layers=L, device=dev, seed=5, tree_seed=5)
-    g = torch.Generator(device=dev)
-    g.manual_seed(5)
-
-    def w(*shape):
-        return (torch.randn(shape, generator=g, device=dev) * 0.02).to(torch.bfloat16)
-
-    # nn.Linear weight layout [out_features, in_features], applied as x @ W.T
-    layers = [dict(qkv=w((H + 2 * Hk) * D, hid), o=w(hid, H * D), gu=w(2 * F, hid), d=w(hid, F)) for _ in range(L)]
-    lm_head = w(V, hid)  # nn.Linear(hid, V).weight layout
-    x0 = w(M, hid) * 50
-    par = torch.tensor(inp.parent, dtype=torch.int64, device=dev)
-    pref = torch.tensor([[p - 1 for p in inp.parent[1:]]], dtype=torch.int64, device=dev)
-    pos = torch.tensor([N + d for d in inp.depth], dtype=torch.int64, device=dev)
-    draft = torch.randint(0, V, (1, M), generator=g, device=dev)
-    # RoPE tables at the nodes' positions; tree tokens occupy logical slots [N, N+M).
-    inv = 1.0 / (5e5 ** (torch.arange(0, D, 2, device=dev, dtype=torch.float32) / D))
-    ang = pos.float()[:, None] * inv[None, :]
-    cos = torch.cat([ang.cos(), ang.cos()], -1).to(torch.bfloat16)
-    sin = torch.cat([ang.sin(), ang.sin()], -1).to(torch.bfloat16)
-    tok = torch.arange(N, N + M, device=dev)
-    phys = inp.page_table.long()[tok // inp.page_size]
-    slot = tok % inp.page_size
-
-    def rms(t):
-        tf = t.float()
-        return (tf * torch.rsqrt(tf.pow(2).mean(-1, keepdim=True) + 1e-5)).to(torch.bfloat16)
-
-    def rope_ref(t):  # the reference's op sequence on [M, heads, D]
-        c, s_ = cos[:, None, :], sin[:, None, :]
-        return (t * c) + (torch.cat((-t[..., D // 2:], t[..., :D // 2]), -1) * s_)
-
-    def step():
-        x = x0
-        for l in range(L):
-            W = layers[l]
-            qkv = rms(x) @ W["qkv"].T
-            q = append_tree_kv(qkv[:, H * D:(H + Hk) * D].view(M, Hk, D), qkv[:, (H + Hk) * D:].view(M, Hk, D),
-                               inp.kv_pages[l, 0], inp.kv_pages[l, 1], N, cos=cos, sin=sin,
-                               page_table=inp.page_table, q=qkv[:, :H * D].view(M, H, D))
-            o, _ = tree_verify(q.unsqueeze(0), inp.kv_pages[l, 0], inp.kv_pages[l, 1], N, par,
-                               page_table=inp.page_table)
-            x = x + o.view(M, H * D) @ W["o"].T
-            gu = rms(x) @ W["gu"].T
-            x = x + (torch.nn.functional.silu(gu[:, :F].float()) * gu[:, F:].float()).to(torch.bfloat16) @ W["d"].T
-        # lm_head fused with the greedy acceptance (kernel 5 + the walk)
-        return lmhead_tree_accept(rms(x).unsqueeze(0), lm_head, draft, pref, pos, 10)
-
+    st = wl.LlamaVerifyStep(device="cuda")
+    path = st.plant_path()
+    inp, N, M, L, H, Hk, D = st.inp, st.N, st.M, st.L, st.H, st.Hk, st.D
     for _ in range(3):
-        step()
+        r = st.step()
     torch.cuda.synchronize()
     n = 10
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(n):
-        r = step()
+        r = st.step()
     e1.record()
     torch.cuda.synchronize()
     us_eager = e0.elapsed_time(e1) / n * 1e3
     # Device time of the step: the whole 32-layer step captured in a HIP graph
     # and replayed (Python launch overhead excluded; eager launching leaves the
     # GPU idle between this scaffolding's small torch ops).
-    us_step = device_us(step, calls=1, reps=5)
+    us_step = device_us(st.step, calls=1, reps=5)
     # Attention's device time: one layer's fused verify (kernels 1 and 3),
     # replayed, times the 32 layers.
-    attn_one = device_us(lambda: tree_verify(inp.q, inp.kv_pages[0, 0], inp.kv_pages[0, 1], N, par,
+    attn_one = device_us(lambda: tree_verify(inp.q, inp.kv_pages[0, 0], inp.kv_pages[0, 1], N, st.par,
                                              page_table=inp.page_table), calls=10, reps=10)
     attn_us = L * attn_one
     commit = bench_commit(inp, N, M, L, Hk, D, n)
     # The append alone (one layer): q/k RoPE + tree K/V into the pages, one
     # launch, against the reference's ops (RoPE of q and k in bf16 torch ops,
     # then the K/V writes into the pages).
-    qkv = rms(x0) @ layers[0]["qkv"].T
+    x0 = st.embed[st.draft[0]]
+    qkv = st.rms(x0) @ st.layers[0]["qkv"].T
     qs, ks, vs = (qkv[:, :H * D].view(M, H, D), qkv[:, H * D:(H + Hk) * D].view(M, Hk, D),
                   qkv[:, (H + Hk) * D:].view(M, Hk, D))
+    tok = torch.arange(N, N + M, device="cuda")
+    phys = inp.page_table.long()[tok // inp.page_size]
+    slot = tok % inp.page_size
+
+    def rope_ref(t):  # the reference's op sequence on [M, heads, D]
+        c, s_ = st.cos[:, None, :], st.sin[:, None, :]
+        return (t * c) + (torch.cat((-t[..., D // 2:], t[..., :D // 2]), -1) * s_)
 
     def ours():
-        append_tree_kv(ks, vs, inp.kv_pages[0, 0], inp.kv_pages[0, 1], N, cos=cos, sin=sin,
+        append_tree_kv(ks, vs, inp.kv_pages[0, 0], inp.kv_pages[0, 1], N, cos=st.cos, sin=st.sin,
                        page_table=inp.page_table, q=qs)
 
     def theirs():
@@ -353,45 +314,58 @@ def bench_llama8b_step(args, lib, ev):
 
     app = {"us": round(device_us(ours), 2), "reference_ops_us": round(device_us(theirs), 2),
            "timing": "device time per call, HIP graph of 10 calls replayed"}
-    lmh = bench_lmhead(lm_head, x0, draft, pref, pos, rms)
-    wbytes = sum(t.numel() * 2 for W in layers for t in W.values()) + lm_head.numel() * 2
+    lmh = bench_lmhead(st)
+    wbytes = sum(t.numel() * 2 for W in st.layers for t in W.values()) + st.lm_head.numel() * 2
     kvbytes = L * algorithmic_bytes(N, M, H, Hk, D)["prefix_kv"]
+    alen = int(r["info"][0, 1])
     return {"workload": "Llama-3.1-8B-shaped verify step: 32 layers, 64-node tree, 65536-token paged prefix per "
-                        "layer, random bf16 weights, lm_head + greedy acceptance",
+                        "layer, random bf16 weights, draft planted along a root path, lm_head + greedy acceptance",
             "us_per_step": round(us_step, 1), "us_per_step_eager": round(us_eager, 1),
             "timing": "us_per_step: device time of the step, HIP graph replayed; us_per_step_eager: eager "
                       "launches (host-bound: the torch scaffolding's launches leave the GPU idle)",
             "attention_us_per_step": round(attn_us, 1), "attention_share": round(attn_us / us_step, 3),
             "weight_bytes": wbytes, "kv_bytes": kvbytes,
             "hbm_gbs": round((wbytes + kvbytes) / (us_step * 1e-6) / 1e9, 1),
-            "accept_length": int(r["info"][0, 1]),
-            "tokens_per_s": round((int(r["info"][0, 1]) + 1) / (us_step * 1e-6), 1),
+            "planted_path_len": len(path), "accept_length": alen,
+            "tokens_per_s": round((alen + 1) / (us_step * 1e-6), 1),
             "lmhead_accept_share": round(lmh["fused_us"] / us_step, 4), "kv_commit": commit,
             "kv_append_one_layer": dict(app, bytes=(M * (H + 2 * Hk) * D * 2) * 2), "lmhead_accept": lmh}
 
 
-def bench_lmhead(lm_head, x0, draft, pref, pos, rms):
+def bench_lmhead(st):
     """lm_head + greedy acceptance of a 64-node tree (Dm 4096, V 128256):
     the fused kernel against torch's lm_head (hipBLASLt, x @ W^T) followed by
-    kernel 4 on the materialised bf16 logits."""
+    kernel 4 on the materialised bf16 logits.  Agreement of the fused walk
+    with the walk over torch's logits is counted over 8 seeds of hidden
+    states (per-node next tokens, and whole results: path, tokens, info)."""
     from diffspec_mi355x.draft.tree_verification import lmhead_tree_accept, tree_accept
 
-    xn = rms(x0)
-    V, hid = lm_head.shape
+    xn = st.rms(st.embed[st.draft[0]])
+    V, hid = st.lm_head.shape
     M = xn.shape[0]
-    fused = device_us(lambda: lmhead_tree_accept(xn.unsqueeze(0), lm_head, draft, pref, pos, 10), calls=5, reps=10)
-    mm = device_us(lambda: xn @ lm_head.T, calls=5, reps=10)
-    unfused = device_us(lambda: tree_accept((xn @ lm_head.T).unsqueeze(0), draft, pref, pos, 10), calls=5, reps=10)
+    args = (st.draft, st.pref, st.pos, st.max_hops)
+    fused = device_us(lambda: lmhead_tree_accept(xn.unsqueeze(0), st.lm_head, *args), calls=5, reps=10)
+    mm = device_us(lambda: xn @ st.lm_head.T, calls=5, reps=10)
+    unfused = device_us(lambda: tree_accept((xn @ st.lm_head.T).unsqueeze(0), *args), calls=5, reps=10)
     nb = V * hid * 2 + M * hid * 2
-    rf = lmhead_tree_accept(xn.unsqueeze(0), lm_head, draft, pref, pos, 10, return_next=True)
-    ru = tree_accept((xn @ lm_head.T).unsqueeze(0), draft, pref, pos, 10, return_next=True)
-    same_next = float((rf["next"] == ru["next"]).float().mean())
+    same_next, same_walk, nodes = 0, 0, 0
+    g = torch.Generator(device="cuda")
+    for seed in range(8):
+        g.manual_seed(100 + seed)
+        h = st.rms(torch.randn((M, hid), generator=g, device="cuda").to(torch.bfloat16))
+        rf = lmhead_tree_accept(h.unsqueeze(0), st.lm_head, *args, return_next=True)
+        ru = tree_accept((h @ st.lm_head.T).unsqueeze(0), *args, return_next=True)
+        same_next += int((rf["next"] == ru["next"]).sum())
+        nodes += M
+        same_walk += int(torch.equal(rf["info"], ru["info"]) and torch.equal(rf["path"], ru["path"])
+                         and torch.equal(rf["tokens"], ru["tokens"]))
     return {"workload": "lm_head [128256 x 4096] bf16 over 64 tree nodes + greedy walk",
             "fused_us": round(fused, 2), "torch_lm_head_us": round(mm, 2),
             "torch_lm_head_plus_kernel4_us": round(unfused, 2), "bytes": nb,
             "fused_hbm_gbs": round(nb / (fused * 1e-6) / 1e9, 1),
             "fused_hbm_frac": round(nb / (fused * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-            "next_token_agreement_with_torch_logits": same_next,
+            "next_token_agreement_with_torch_logits": round(same_next / nodes, 4),
+            "walk_agreement_with_torch_logits": f"{same_walk}/8 seeds",
             "timing": "device time per call, HIP graph of 5 calls replayed"}
 
 

@@ -15,7 +15,7 @@ verification path relies on).
 from __future__ import annotations
 
 from dataclasses import dataclass
-from typing import List, Optional, Tuple
+from typing import Dict, List, Optional, Sequence, Tuple
 
 import numpy as np
 import torch
@@ -171,3 +171,117 @@ def make_accept_inputs(T: int = 8, M: int = 64, V: int = 128256, dtype=torch.bfl
     pos = torch.tensor([[pos_offset + d for d in dep] for dep in depths], dtype=torch.int64, device=device)
     return AcceptInputs(logits=logits, draft=torch.from_numpy(draft).to(device), parent_ref=pref, pos=pos,
                         parents=parents, depths=depths, planted_len=plens)
+
+
+# ----------------------------------------------------------------------------
+# Llama-3.1-8B-shaped verification step
+# ----------------------------------------------------------------------------
+
+class LlamaVerifyStep:
+    """One target-side verification step of a Llama-3.1-8B-shaped model over a
+    draft tree, with seeded random weights (no checkpoint exists offline).
+
+    Shape: ``layers`` decoder layers (32), hidden 4096, 32 query / 8 KV heads
+    of 128, FFN 14336, vocab 128256, RoPE theta 5e5, bf16 weights N(0, 0.02).
+    Every layer's K/V prefix (``n_prefix`` tokens) sits in a page pool behind
+    a random-permutation page table; the tree's K/V follow it in the same
+    pages.  The tree nodes' inputs are their draft tokens' embeddings.
+
+    Per layer (llama_target_model.py:834-867 around the hot path): RMSNorm,
+    QKV projection, RoPE of q and k at the nodes' positions with the tree K/V
+    written into the pages (dsv_kv_append), the fused tree verify (kernels 1
+    and 3), o_proj, RMSNorm, SwiGLU MLP; then the final norm and the lm_head
+    with the greedy walk (draft/diffspec_model.py:229-231 and
+    draft/tree_verification.py:100-182).  Projections, norms and the MLP are
+    torch ops (hipBLASLt GEMMs): scaffolding around the hot path.
+    """
+
+    def __init__(self, n_prefix: int = 65536, M: int = 64, layers: int = 32, hidden: int = 4096, H: int = 32,
+                 Hk: int = 8, D: int = 128, ffn: int = 14336, vocab: int = 128256, theta: float = 5e5,
+                 seed: int = 5, device: str = "cuda"):
+        self.N, self.M, self.L, self.hid, self.H, self.Hk, self.D, self.F, self.V = (
+            n_prefix, M, layers, hidden, H, Hk, D, ffn, vocab)
+        self.dev = device
+        self.inp = make_tree_verify_inputs(n_prefix=n_prefix, M=M, H=H, Hk=Hk, D=D, layers=layers, device=device,
+                                           seed=seed, tree_seed=seed)
+        g = torch.Generator(device=device)
+        g.manual_seed(seed)
+
+        def w(*shape):
+            return (torch.randn(shape, generator=g, device=device) * 0.02).to(torch.bfloat16)
+
+        # nn.Linear weight layout [out_features, in_features], applied as x @ W.T
+        self.layers = [dict(qkv=w((H + 2 * Hk) * D, hidden), o=w(hidden, H * D), gu=w(2 * ffn, hidden),
+                            d=w(hidden, ffn)) for _ in range(layers)]
+        self.lm_head = w(vocab, hidden)
+        # token embeddings at the scale of a trained model's (unit-RMS rows)
+        self.embed = w(vocab, hidden) * 50
+        self.par = torch.tensor(self.inp.parent, dtype=torch.int64, device=device)
+        self.pref = torch.tensor([parent_to_reference(self.inp.parent)], dtype=torch.int64, device=device)
+        self.pos = torch.tensor([n_prefix + d for d in self.inp.depth], dtype=torch.int64, device=device)
+        self.draft = torch.randint(0, vocab, (1, M), generator=g, device=device)
+        inv = 1.0 / (theta ** (torch.arange(0, D, 2, device=device, dtype=torch.float32) / D))
+        ang = self.pos.float()[:, None] * inv[None, :]
+        self.cos = torch.cat([ang.cos(), ang.cos()], -1).to(torch.bfloat16)
+        self.sin = torch.cat([ang.sin(), ang.sin()], -1).to(torch.bfloat16)
+        self.max_hops = min(max(self.inp.depth) + 2, M)
+
+    @staticmethod
+    def rms(t: torch.Tensor) -> torch.Tensor:
+        tf = t.float()
+        return (tf * torch.rsqrt(tf.pow(2).mean(-1, keepdim=True) + 1e-5)).to(torch.bfloat16)
+
+    def hidden(self, capture: Sequence[int] = ()) -> Tuple[torch.Tensor, Dict[int, Tuple[torch.Tensor, torch.Tensor]]]:
+        """The 32 layers over the tree; returns the final normed hidden states
+        [M, hidden] and, for the layers in ``capture``, (rotated q [M, H, D],
+        attention output [M, H, D])."""
+        from .runtime.cache_state import append_tree_kv
+        from .runtime.tree_attention import tree_verify
+
+        M, H, Hk, D, F, N = self.M, self.H, self.Hk, self.D, self.F, self.N
+        inp = self.inp
+        caps = {}
+        x = self.embed[self.draft[0]]
+        for l in range(self.L):
+            W = self.layers[l]
+            qkv = self.rms(x) @ W["qkv"].T
+            q = append_tree_kv(qkv[:, H * D:(H + Hk) * D].view(M, Hk, D), qkv[:, (H + Hk) * D:].view(M, Hk, D),
+                               inp.kv_pages[l, 0], inp.kv_pages[l, 1], N, cos=self.cos, sin=self.sin,
+                               page_table=inp.page_table, q=qkv[:, :H * D].view(M, H, D))
+            o, _ = tree_verify(q.unsqueeze(0), inp.kv_pages[l, 0], inp.kv_pages[l, 1], N, self.par,
+                               page_table=inp.page_table)
+            if l in capture:
+                caps[l] = (q.clone(), o[0].clone())
+            x = x + o.view(M, H * D) @ W["o"].T
+            gu = self.rms(x) @ W["gu"].T
+            x = x + (torch.nn.functional.silu(gu[:, :F].float()) * gu[:, F:].float()).to(torch.bfloat16) @ W["d"].T
+        return self.rms(x), caps
+
+    def step(self) -> Dict[str, torch.Tensor]:
+        """The whole verification step: layers, then the lm_head fused with the
+        greedy walk (kernel 5 + kernel 4's walk)."""
+        from .draft.tree_verification import lmhead_tree_accept
+
+        xn, _ = self.hidden()
+        return lmhead_tree_accept(xn.unsqueeze(0), self.lm_head, self.draft, self.pref, self.pos, self.max_hops)
+
+    def torch_logits(self, xn: torch.Tensor) -> torch.Tensor:
+        """The reference's bf16 lm_head logits [1, M, V] (nn.Linear: x @ W.T)."""
+        return (xn @ self.lm_head.T).unsqueeze(0)
+
+    def plant_path(self, node: Optional[int] = None) -> List[int]:
+        """Make the draft agree with the target along the root path of ``node``
+        (default: the first deepest node), top-down: the token of each path
+        node becomes the argmax of torch's logits at its parent, whose hidden
+        state depends only on tokens already fixed.  One pass of the layers per
+        edge.  Returns the path (root first)."""
+        if node is None:
+            node = int(np.argmax(self.inp.depth))
+        path = [node]
+        while path[-1] > 0:
+            path.append(self.inp.parent[path[-1]])
+        path.reverse()
+        for par, child in zip(path[:-1], path[1:]):
+            xn, _ = self.hidden()
+            self.draft[0, child] = int(torch.argmax(self.torch_logits(xn)[0, par].float()))
+        return path

@@ -1,0 +1,70 @@
+"""The Llama-3.1-8B-shaped verification step end to end (32 layers, hidden
+4096, GQA 32/8, head_dim 128, FFN 14336, vocab 128256, RoPE theta 5e5, random
+bf16 weights N(0, 0.02), a 65536-token paged prefix per layer, a 64-node
+tree), with the draft planted along a root path from the target's own argmax
+so the walk has something to accept.
+
+Checked:
+  * the fused tree verify of the first, a middle and the last layer, on that
+    layer's own rotated q and paged K/V, all 32 heads, against the fp64 oracle
+    (llama_target_model.py:834-867);
+  * the walk (kernel 4) over torch's bf16 lm_head logits of the final hidden
+    states, bit-exact against the oracle walk (draft/tree_verification.py:100-182);
+  * the fused lm_head + walk (kernel 5) against the same: equal next tokens
+    wherever torch's own top two logits are more than a rounding step apart.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import accept as oacc
+from oracle import attention as oa
+from diffspec_mi355x import workloads as wl
+from diffspec_mi355x.draft.tree_verification import lmhead_tree_accept, tree_accept
+
+pytestmark = pytest.mark.gpu
+
+
+def np64(t):
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+def test_llama8b_shaped_verify_step(gpu):
+    print("[llama step] building (32 layers, 64K paged prefix per layer)", flush=True)
+    st = wl.LlamaVerifyStep(device=str(gpu))
+    path = st.plant_path()
+    print(f"[llama step] planted path {path}", flush=True)
+    xn, caps = st.hidden(capture=(0, 15, 31))
+    torch.cuda.synchronize()
+    for l, (q, o) in caps.items():
+        print(f"[llama step] layer {l} attention vs oracle", flush=True)
+        k = np64(st.inp.logical_kv(l, 0)[0])
+        v = np64(st.inp.logical_kv(l, 1)[0])
+        o_ref, _ = oa.tree_verify(np64(q), k, v, st.N, st.inp.parent)
+        got = np64(o)
+        diff = np.abs(got - o_ref)
+        rel = np.linalg.norm(got - o_ref) / np.linalg.norm(o_ref)
+        assert diff.max() <= 2e-2 and diff.mean() <= 2e-3 and rel <= 1e-2, (l, diff.max(), diff.mean(), rel)
+
+    logits = st.torch_logits(xn)
+    max_depth = max(st.inp.depth)
+    r = tree_accept(logits, st.draft, st.pref, st.pos, st.max_hops, return_next=True)
+    lg = logits[0].float().cpu().numpy()
+    w_toks, w_ids, w_alen, w_next, w_id = oacc.greedy_walk(lg, st.draft[0].cpu().numpy(), st.pref[0].tolist(),
+                                                           st.pos.cpu().numpy(), max_depth)
+    info = r["info"][0].cpu().tolist()
+    assert info == [w_id, w_alen, w_next, len(w_ids)]
+    assert r["path"][0, :len(w_ids)].cpu().tolist() == w_ids
+    assert r["tokens"][0, :len(w_ids)].cpu().tolist() == w_toks
+    assert w_alen >= len(path) - 1  # the planted path is accepted
+
+    rf = lmhead_tree_accept(xn.unsqueeze(0), st.lm_head, st.draft, st.pref, st.pos, st.max_hops, return_next=True)
+    nf, nt = rf["next"][0].cpu().numpy(), r["next"][0].cpu().numpy()
+    top2 = np.sort(lg, axis=-1)[:, -2:]
+    step = np.exp2(np.floor(np.log2(np.abs(top2[:, 1]))) - 7)  # one bf16 step at the top logit
+    near_tie = (top2[:, 1] - top2[:, 0]) <= 2 * step
+    assert np.all((nf == nt) | near_tie), np.nonzero((nf != nt) & ~near_tie)
+    if np.array_equal(nf, nt):
+        assert torch.equal(rf["info"], r["info"]) and torch.equal(rf["path"], r["path"])
+    print(f"[llama step] accept_length {w_alen}, next-token agreement {np.mean(nf == nt):.3f}", flush=True)
