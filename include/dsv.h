@@ -214,6 +214,28 @@ int dsv_tree_verify(const dsv_tensor* q, const dsv_tensor* k,
                     dsv_tensor* lse, void* workspace, size_t workspace_bytes,
                     void* stream);
 
+/*
+ * dsv_tree_verify without a workspace, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No reference counterpart.  The split
+ * partials live in a fixed per-GPU device array of DSV_NOALLOC_SCRATCH_BYTES
+ * that the library holds until the process ends; shapes whose split plan
+ * needs more fail with DSV_ERR_UNSUPPORTED (dsv_attn_workspace_bytes gives
+ * the need; at head_dim 128 with 8 KV heads on 256 CUs: one tree of <= 64
+ * nodes up to 512K prefix tokens, <= 128 nodes up to 256K, <= 256 nodes up
+ * to 128K, 8 trees of 64 nodes at 64K).  The call allocates nothing.  Every
+ * call on one
+ * GPU shares that GPU's array: calls that overlap in time on one GPU (other
+ * streams, other threads) race and must be serialised by the caller.
+ * Arguments and results are those of dsv_tree_verify.
+ */
+#define DSV_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+int dsv_tree_verify_noalloc(const dsv_tensor* q, const dsv_tensor* k,
+                            const dsv_tensor* v, const dsv_tensor* page_table,
+                            int64_t n_prefix, const dsv_tensor* parent,
+                            const dsv_tensor* row_perm, dsv_tensor* out,
+                            dsv_tensor* lse, void* stream);
+
 /* ------------------------------------------------------------------------- */
 /* Acceptance (kernel 4)                                                      */
 /* ------------------------------------------------------------------------- */

@@ -10,6 +10,7 @@
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 namespace dsv {
@@ -620,9 +621,45 @@ int dsv_verify_bundle_paged(const dsv_tensor* q, const dsv_tensor* kv_pages, con
 
 namespace {
 
+// Scratch of the allocation-free tree verify: a file-scope device array, one
+// copy per GPU for the life of the process.  The split plan fills the GPU's
+// workgroup slots with (batch, KV head, row block, split) units and needs
+// 2 * D + 8 bytes per (split, batch, KV head, query row), about
+// slots x 256 rows x (2 * D + 8) bytes (17 MiB at D = 128 on 256 CUs) until
+// the 16384-key cap on a split adds splits.  At D = 128, 8 KV heads, 256 CUs
+// 32 MiB holds one tree of <= 64 nodes up to 512K prefix tokens, <= 128
+// nodes up to 256K, <= 256 nodes up to 128K, and 8 trees of 64 nodes at 64K.
+constexpr size_t kNoAllocScratchBytes = DSV_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of this GPU's scratch array, looked up once per device with
+// that device current (the array's name is a host-side stand-in and may not
+// be passed to a kernel or a copy).
+int scratch_for_current_device(void** ptr) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(DSV_ERR_UNSUPPORTED, "device ordinal %d beyond %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (p == nullptr || (reinterpret_cast<uintptr_t>(p) & 255) != 0)
+      return fail(DSV_ERR_HIP, "scratch array at an unusable address");
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return DSV_OK;
+}
+
 int tree_verify_impl(const dsv_tensor* q, const dsv_tensor* k, const dsv_tensor* v, const dsv_tensor* page_table,
                      int64_t n_prefix, const dsv_tensor* parent, const dsv_tensor* row_perm, dsv_tensor* out,
-                     dsv_tensor* lse, void* workspace, size_t workspace_bytes, void* stream) {
+                     dsv_tensor* lse, void* workspace, size_t workspace_bytes, bool noalloc, void* stream) {
   int rc;
   if ((rc = check_q_out(q, out)) != DSV_OK) return rc;
   const int64_t B = q->shape[0], M = q->shape[1], H = q->shape[2], D = q->shape[3];
@@ -694,6 +731,15 @@ int tree_verify_impl(const dsv_tensor* q, const dsv_tensor* k, const dsv_tensor*
       return fail(DSV_ERR_INVALID, "lse must be float32 [B, M, H]");
   }
   const Plan p = make_plan(B, M, H, Hk, D, n_prefix, ps, true);
+  if (noalloc) {
+    if (p.total > kNoAllocScratchBytes)
+      return fail(DSV_ERR_UNSUPPORTED,
+                  "this shape needs %zu bytes of split scratch, above the %zu bytes of the allocation-free entry "
+                  "point; use dsv_tree_verify with a workspace",
+                  p.total, kNoAllocScratchBytes);
+    if ((rc = scratch_for_current_device(&workspace)) != DSV_OK) return rc;
+    workspace_bytes = kNoAllocScratchBytes;
+  }
   if ((rc = check_ws(p, workspace, workspace_bytes)) != DSV_OK) return rc;
 
   AttnArgs a{};
@@ -735,9 +781,14 @@ int dsv_tree_verify(const dsv_tensor* q, const dsv_tensor* k, const dsv_tensor* 
                     int64_t n_prefix, const dsv_tensor* parent, const dsv_tensor* row_perm, dsv_tensor* out,
                     dsv_tensor* lse, void* workspace, size_t workspace_bytes, void* stream) {
   return tree_verify_impl(q, k, v, page_table, n_prefix, parent, row_perm, out, lse, workspace, workspace_bytes,
-                          stream);
+                          false, stream);
 }
 
+int dsv_tree_verify_noalloc(const dsv_tensor* q, const dsv_tensor* k, const dsv_tensor* v,
+                            const dsv_tensor* page_table, int64_t n_prefix, const dsv_tensor* parent,
+                            const dsv_tensor* row_perm, dsv_tensor* out, dsv_tensor* lse, void* stream) {
+  return tree_verify_impl(q, k, v, page_table, n_prefix, parent, row_perm, out, lse, nullptr, 0, true, stream);
+}
 
 // ----------------------------------------------------------------------------
 // Acceptance

@@ -64,6 +64,7 @@ SIGNATURES = {
     "dsv_verify_bundle": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _V, _SZ, _V]),
     "dsv_verify_bundle_paged": (ctypes.c_int, [_P, _P, _P, _I64, _P, _P, _P, _V, _SZ, _V]),
     "dsv_tree_verify": (ctypes.c_int, [_P, _P, _P, _P, _I64, _P, _P, _P, _P, _V, _SZ, _V]),
+    "dsv_tree_verify_noalloc": (ctypes.c_int, [_P, _P, _P, _P, _I64, _P, _P, _P, _P, _V]),
     "dsv_accept_workspace_bytes": (_SZ, [_I64, _I64, _I64]),
     "dsv_tree_accept": (
         ctypes.c_int,
