@@ -272,6 +272,34 @@ int dsv_tree_accept(int mode, const dsv_tensor* logits, const dsv_tensor* draft,
                     dsv_tensor* out_info, dsv_tensor* out_next,
                     void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Sampling acceptance — the logits_processor branch of verify_new
+ * (draft/tree_verification.py:103-106: warp, softmax, one multinomial draw
+ * per node, then the walk of :108-182) with the warpers of
+ * prepare_logits_processor (:15-32).  y = logits / temperature rounded to the
+ * logits dtype (temperature == 1: unchanged); top-p (applied when
+ * 1e-8 <= top_p < 1) keeps the head of the order "descending y, then
+ * descending index" whose probability mass reaches top_p, the masses taken
+ * as exact 64-bit fixed-point integers; top-k (applied when > 0) keeps
+ * y >= the k-th largest y.  The draw per node is a counter-based Gumbel-max
+ * over the kept tokens: argmax of y + G, G = -ln(-ln U), U from
+ * Philox4x64-10 with key (seed, 0) and counter (token, node, tree, 0), the
+ * logarithms evaluated with a fixed sequence of correctly rounded double
+ * operations, so the draws are reproducible bit for bit; they are samples of
+ * softmax(y) over the kept set.  A row without a finite logit draws token 0.
+ *   logits, draft, parent, pos, max_hops, out_*: as dsv_tree_accept;
+ *   out_next receives the per-node draws.  temperature >= 1e-5 (the
+ *   reference takes the greedy branch below it).  Workspace:
+ *   dsv_accept_workspace_bytes.
+ */
+int dsv_tree_accept_sample(const dsv_tensor* logits, const dsv_tensor* draft,
+                           const dsv_tensor* parent, const dsv_tensor* pos,
+                           int64_t max_hops, float temperature, float top_p,
+                           int64_t top_k, uint64_t seed, dsv_tensor* out_path,
+                           dsv_tensor* out_tokens, dsv_tensor* out_info,
+                           dsv_tensor* out_next, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------- */
 /* Accepted-path KV commit                                                    */
 /* ------------------------------------------------------------------------- */

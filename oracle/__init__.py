@@ -11,6 +11,8 @@ Modules
                 the typical (posterior) walk and an independent brute force
   bundles       restatement of the bundle scheduler (core/bundle_scheduler.py:42-171)
                 and the query packing order built from it
+  sampling      the sampling branch of verify_new (draft/tree_verification.py:103-106
+                with the warpers of :15-32) as a seeded counter-based Gumbel-max draw
   ref_cpu_path  the reference's own torch CPU op sequence (repeat_kv -> prefix
                 matmul/softmax/logsumexp -> naive tree -> sigmoid merge -> walk),
                 timed as the CPU baseline
@@ -24,6 +26,11 @@ Pinning (what each function is checked against, besides the GPU):
                         full accept, root only) — tests/test_oracle_accept.py
   bundles.packing_order the reference's scheduler vectors, hand-worked orders,
                         invariants on generated trees — tests/test_oracle_bundles.py
+  sampling              numpy.random.Philox (the counter RNG), numpy's log/exp2
+                        (the deterministic ln / 2^x), transformers' own warpers on
+                        committed fixture rows (tests/golden/sampling_warpers.json),
+                        an independent float nucleus, chi-square of the draws
+                        against the softmax — tests/test_oracle_sampling.py
   typical_walk          closed forms of the entropy (uniform, one-hot) and the
                         greedy/typical relation on planted cases.  The reference
                         has no typical acceptance: parity with the reference is

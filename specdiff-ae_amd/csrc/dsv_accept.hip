@@ -501,7 +501,23 @@ __global__ void __launch_bounds__(1024) accept_walk_kernel(const AcceptArgs a) {
     float bv = kNegInf;
     int bi = -1;
     Soft sm{kNegInf, 0.f, 0.f};
-    for (int c0 = 0; c0 < a.nchunk; c0 += 4) {
+    if (a.mode == 2) {
+      // Sampling: the ranges' Gumbel-max draws (z as a double, index; -1 =
+      // nothing kept); the largest z wins, then the lowest index.
+      double bz = 0.0;
+      for (int c = 0; c < a.nchunk; ++c) {
+        const float4 st = a.rstat[row * a.nchunk + c];
+        const int ci = __float_as_int(st.z);
+        const double z = __builtin_bit_cast(
+            double, (uint64_t)__float_as_uint(st.x) | ((uint64_t)__float_as_uint(st.y) << 32));
+        if (ci >= 0 && (bi < 0 || z > bz || (z == bz && ci < bi))) {
+          bz = z;
+          bi = ci;
+        }
+      }
+      if (bi < 0) bi = 0;
+    }
+    for (int c0 = 0; a.mode != 2 && c0 < a.nchunk; c0 += 4) {
       float4 st[4];
       float s2[4];
 #pragma unroll
@@ -567,7 +583,7 @@ __global__ void __launch_bounds__(1024) accept_walk_kernel(const AcceptArgs a) {
     int ok = 1;
     if (i > 0) {
       const int p = par[i];
-      if (a.mode == 0) {
+      if (a.mode != 1) {
         ok = (tok == (int64_t)nxt[p]);
       } else {
         ok = 0;
@@ -806,6 +822,10 @@ hipError_t launch_accept(const AcceptArgs& a, hipStream_t s, hipEvent_t ev0, hip
     e = launch_rowstat<float>(a, s);
   if (e != hipSuccess) return e;
   if (ev1 != nullptr && (e = hipEventRecord(ev1, s)) != hipSuccess) return e;
+  return launch_walk(a, s);
+}
+
+hipError_t launch_walk(const AcceptArgs& a, hipStream_t s) {
   const int threads = ((a.M + 63) / 64) * 64;
   hipLaunchKernelGGL(accept_walk_kernel, dim3((unsigned)a.T), dim3(threads), accept_walk_lds_bytes(a.M), s, a);
   return hipGetLastError();

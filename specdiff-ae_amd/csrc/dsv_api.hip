@@ -8,6 +8,7 @@
 #include "dsv_internal.h"
 
 #include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <mutex>
@@ -797,7 +798,9 @@ int dsv_tree_verify_noalloc(const dsv_tensor* q, const dsv_tensor* k, const dsv_
 size_t dsv_accept_workspace_bytes(int64_t T, int64_t M, int64_t V) {
   if (T <= 0 || M <= 0 || V <= 0) return 0;
   const size_t rows = (size_t)T * M * dsv::accept_max_chunks(V);
-  return align_up(rows * 16, 256) + align_up(rows * 4, 256);
+  // per (row, range) statistics, the typical sums, and per row the sampling
+  // mode's kept-set bounds
+  return align_up(rows * 16, 256) + align_up(rows * 4, 256) + align_up((size_t)T * M * 16, 256);
 }
 
 int dsv_kv_append(const dsv_tensor* k, const dsv_tensor* v, const dsv_tensor* cos, const dsv_tensor* sin,
@@ -1224,6 +1227,57 @@ int dsv_tree_accept(int mode, const dsv_tensor* logits, const dsv_tensor* draft,
   take_events(ev0, ev1);
   hipError_t e = dsv::launch_accept(a, static_cast<hipStream_t>(stream), ev0, ev1);
   if (e != hipSuccess) return hip_fail(e, "acceptance kernel launch");
+  return DSV_OK;
+}
+
+int dsv_tree_accept_sample(const dsv_tensor* logits, const dsv_tensor* draft, const dsv_tensor* parent,
+                           const dsv_tensor* pos, int64_t max_hops, float temperature, float top_p, int64_t top_k,
+                           uint64_t seed, dsv_tensor* out_path, dsv_tensor* out_tokens, dsv_tensor* out_info,
+                           dsv_tensor* out_next, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc;
+  if ((rc = check_nd(logits, "logits", 3)) != DSV_OK) return rc;
+  if (logits->dtype != DSV_BF16 && logits->dtype != DSV_F16 && logits->dtype != DSV_F32)
+    return fail(DSV_ERR_INVALID, "logits must be bf16, f16 or f32");
+  if (logits->stride[2] != 1) return fail(DSV_ERR_INVALID, "logits vocab stride must be 1");
+  if (!(temperature >= 1e-5f) || !(temperature < __builtin_huge_valf()))
+    return fail(DSV_ERR_INVALID, "temperature must be >= 1e-5 (smaller temperatures are greedy acceptance)");
+  if (!(top_p >= 0.f && top_p <= 1.f)) return fail(DSV_ERR_INVALID, "top_p must lie in [0, 1]");
+  if (top_k < 0) return fail(DSV_ERR_INVALID, "top_k must be >= 0");
+  const int64_t T = logits->shape[0], M = logits->shape[1], V = logits->shape[2];
+  AcceptArgs a{};
+  if ((rc = accept_common(DSV_ACCEPT_GREEDY, T, M, V, draft, parent, pos, max_hops, 1.f, 0.f, 0.f, out_path,
+                          out_tokens, out_info, out_next, a)) != DSV_OK)
+    return rc;
+  const size_t need = dsv_accept_workspace_bytes(T, M, V);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(DSV_ERR_WORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace_bytes);
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255) != 0) return fail(DSV_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+
+  a.mode = 2;
+  a.logits = logits->data;
+  a.l_dtype = logits->dtype;
+  a.l_st = logits->stride[0];
+  a.l_sm = logits->stride[1];
+  a.temperature = temperature;
+  // The warpers that apply, as prepare_logits_processor builds them
+  // (draft/tree_verification.py:15-32): top-p when 1e-8 <= top_p < 1, top-k when > 0.
+  a.top_p_q = (top_p >= 1e-8f && top_p < 1.f) ? (uint32_t)std::nearbyint((double)top_p * 4294967296.0) : 0u;
+  a.top_k = top_k;
+  a.seed = seed;
+  dsv::accept_chunking(a, device_cus());
+  const size_t rows = (size_t)T * M * a.nchunk;
+  char* ws = static_cast<char*>(workspace);
+  a.rstat = reinterpret_cast<float4*>(ws);
+  const size_t max_rows = (size_t)T * M * dsv::accept_max_chunks(V);
+  a.sel = (a.top_p_q != 0 || top_k > 0)
+              ? reinterpret_cast<uint4*>(ws + align_up(max_rows * 16, 256) + align_up(max_rows * 4, 256))
+              : nullptr;
+  (void)rows;
+  if (g_dry_run) return DSV_OK;
+  hipEvent_t ev0, ev1;
+  take_events(ev0, ev1);
+  hipError_t e = dsv::launch_sample(a, static_cast<hipStream_t>(stream), ev0, ev1);
+  if (e != hipSuccess) return hip_fail(e, "sampling acceptance launch");
   return DSV_OK;
 }
 

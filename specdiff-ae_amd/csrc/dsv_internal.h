@@ -125,6 +125,12 @@ struct AcceptArgs {
   int64_t* out_info; int64_t oi_st;
   int64_t* out_next; int64_t on_st;
   const float* xtok;       // optional [T*M] draft-token logits under the parent (fused lm_head)
+  // Sampling (mode 2): warpers and the counter-based draw.
+  float temperature;       // y = x / T rounded to the logits dtype (T == 1: y = x)
+  uint32_t top_p_q;        // rint(top_p * 2^32); 0: no top-p
+  int64_t top_k;           // 0: no top-k
+  uint64_t seed;           // Philox key word 0
+  uint4* sel;              // [T*M] kept-set bounds (top-k key, top-p key, top-p index); nullptr: keep all
 };
 
 // Arguments of the accepted-path KV commit.
@@ -215,6 +221,11 @@ int attn_rows_per_block();
 int attn_blocks_per_cu();
 hipError_t launch_merge(const MergeArgs& a, hipStream_t s);
 hipError_t launch_accept(const AcceptArgs& a, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1);
+// Sampling mode: kept-set selection (top-p / top-k), the Gumbel-max draw per
+// vocabulary range, then the walk.
+hipError_t launch_sample(const AcceptArgs& a, hipStream_t s, hipEvent_t ev0, hipEvent_t ev1);
+// The walk of kernel 4 over the per-range statistics already in a.rstat.
+hipError_t launch_walk(const AcceptArgs& a, hipStream_t s);
 // Walk over per-row partial statistics part / part2 ([T*M, nin]) already
 // computed (fused lm_head): combines them into a.rstat / a.rstat2 (one per
 // row, a.nchunk == 1), then runs the walk.

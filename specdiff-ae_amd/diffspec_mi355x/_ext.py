@@ -71,6 +71,10 @@ SIGNATURES = {
         [ctypes.c_int, _P, _P, _P, _P, _I64, ctypes.c_float, ctypes.c_float, ctypes.c_float, _P, _P, _P, _P, _V,
          _SZ, _V],
     ),
+    "dsv_tree_accept_sample": (
+        ctypes.c_int,
+        [_P, _P, _P, _P, _I64, ctypes.c_float, ctypes.c_float, _I64, ctypes.c_uint64, _P, _P, _P, _P, _V, _SZ, _V],
+    ),
     "dsv_kv_commit": (ctypes.c_int, [_P, _P, _I64, _P, _P, _I64, _V]),
     "dsv_kv_append": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _P, _I64, _P, _P, _V]),
     "dsv_bundle_order": (ctypes.c_int, [_P, _I64, _I64, _I64, _P, _P, _V]),

@@ -12,11 +12,17 @@ prepend) follows the reference.
 
 Acceptance modes:
   * ``greedy`` — the reference rule (``logits_processor is None``).
+  * ``sample`` — the reference's sampling branch (``logits_processor`` given,
+    :103-106): the warpers of ``prepare_logits_processor`` (:15-32;
+    temperature, top-p, top-k), one draw per node from softmax of the warped
+    logits, then the same walk.  The draw is a seeded counter-based
+    Gumbel-max (libdsv's dsv_tree_accept_sample) instead of
+    ``torch.multinomial``: same distribution, reproducible from its seed,
+    which ``verify_new`` takes from torch's default generator (so
+    ``torch.manual_seed`` fixes it, as it fixes the reference's draws).
   * ``typical`` — posterior (typical) acceptance of Cai et al. 2024 (Medusa):
     accept node i iff p_T(draft[i] | parent) > min(eps, alpha * exp(-H)),
     with H the entropy of p_T(. | parent); the reference has no such mode.
-The reference's multinomial sampling branch (``logits_processor`` given)
-draws from torch's RNG and is not reproduced; it raises.
 """
 
 from __future__ import annotations
@@ -28,14 +34,71 @@ import torch
 from .. import _ext
 from ..core.bundle_scheduler import BundleScheduler
 
-__all__ = ["tree_accept", "evaluate_tree", "kv_commit", "verify", "verify_new"]
+__all__ = ["tree_accept", "evaluate_tree", "kv_commit", "verify", "verify_new", "prepare_logits_processor",
+           "SamplingParams"]
+
+
+class SamplingParams:
+    """The warpers of the reference's sampling branch: temperature, then top-p,
+    then top-k (prepare_logits_processor, draft/tree_verification.py:15-32)."""
+
+    def __init__(self, temperature: float = 1.0, top_p: float = 1.0, top_k: int = 0):
+        self.temperature, self.top_p, self.top_k = float(temperature), float(top_p), int(top_k)
+
+    def __repr__(self) -> str:
+        return f"SamplingParams(temperature={self.temperature}, top_p={self.top_p}, top_k={self.top_k})"
+
+
+def prepare_logits_processor(temperature: float = 0.0, repetition_penalty: float = 0.0, top_p: float = 0.0,
+                             top_k: int = 0) -> Optional[SamplingParams]:
+    """Mirror of the reference's prepare_logits_processor (:15-32): None (greedy)
+    for temperature <= 1e-5, else the warpers to apply.  The repetition penalty
+    is refused: the reference's only call (:104) passes input_ids=None, which
+    RepetitionPenaltyLogitsProcessor cannot take."""
+    if temperature > 1e-5:
+        if repetition_penalty > 1.0:
+            raise NotImplementedError("the repetition penalty needs the input ids, which verify_new does not pass")
+        return SamplingParams(temperature=temperature if temperature != 1.0 else 1.0,
+                              top_p=top_p if 1e-8 <= top_p < 1.0 else 1.0, top_k=top_k if top_k > 0 else 0)
+    return None
+
+
+def _sampling_params(logits_processor) -> SamplingParams:
+    """SamplingParams from this module's prepare_logits_processor or from the
+    transformers LogitsProcessorList the reference builds (temperature, top-p,
+    top-k warpers in that order)."""
+    if isinstance(logits_processor, SamplingParams):
+        return logits_processor
+    T, p, k, rank = 1.0, 1.0, 0, -1
+    order = {"TemperatureLogitsWarper": 0, "TopPLogitsWarper": 1, "TopKLogitsWarper": 2}
+    for proc in logits_processor:
+        name = type(proc).__name__
+        if name not in order:
+            raise NotImplementedError(f"{name} is not supported by the sampling acceptance kernel")
+        if order[name] <= rank:
+            raise NotImplementedError("the warpers must come in the order temperature, top-p, top-k")
+        rank = order[name]
+        if getattr(proc, "min_tokens_to_keep", 1) != 1 or getattr(proc, "filter_value", float("-inf")) != float("-inf"):
+            raise NotImplementedError(f"{name}: only min_tokens_to_keep=1 and filter_value=-inf are supported")
+        if name == "TemperatureLogitsWarper":
+            T = float(proc.temperature)
+        elif name == "TopPLogitsWarper":
+            p = float(proc.top_p)
+        else:
+            k = int(proc.top_k)
+    return SamplingParams(T, p, k)
 
 
 def tree_accept(logits: torch.Tensor, draft: torch.Tensor, parent: torch.Tensor, pos: torch.Tensor,
                 max_hops: int, mode: str = "greedy", temperature: float = 1.0,
                 posterior_threshold: float = 0.09, posterior_alpha: float = 0.3,
-                return_next: bool = False) -> Dict[str, torch.Tensor]:
+                return_next: bool = False, top_p: float = 1.0, top_k: int = 0,
+                seed: int = 0) -> Dict[str, torch.Tensor]:
     """Batched acceptance of T independent trees (kernel 4).
+
+    ``mode`` is "greedy", "typical" or "sample" (temperature, top_p, top_k and
+    the 64-bit ``seed`` of the counter-based draw; ``next`` then holds the
+    per-node draws).
 
     Args:
         logits: [T, M, V] (or [M, V]) bf16/f16/f32 target logits per node.
@@ -63,17 +126,24 @@ def tree_accept(logits: torch.Tensor, draft: torch.Tensor, parent: torch.Tensor,
         parent = parent.to(torch.int64)
     if pos.dtype != torch.int64:
         pos = pos.to(torch.int64)
-    mode_id = {"greedy": _ext.ACCEPT_GREEDY, "typical": _ext.ACCEPT_TYPICAL}[mode]
     lib = _ext.load()
     path = torch.empty((T, M), dtype=torch.int64, device=dev)
     tokens = torch.empty((T, M), dtype=torch.int64, device=dev)
     info = torch.empty((T, 4), dtype=torch.int64, device=dev)
     nxt = torch.empty((T, M), dtype=torch.int64, device=dev) if return_next else None
     ws = _ext.workspace(lib.dsv_accept_workspace_bytes(T, M, V), dev)
-    rc = lib.dsv_tree_accept(mode_id, _ext.desc(logits), _ext.desc(draft), _ext.desc(parent), _ext.desc(pos),
-                             int(max_hops), float(temperature), float(posterior_threshold), float(posterior_alpha),
-                             _ext.desc(path), _ext.desc(tokens), _ext.desc(info), _ext.desc(nxt),
-                             ws.data_ptr(), ws.numel(), _ext.stream_of(dev))
+    if mode == "sample":
+        rc = lib.dsv_tree_accept_sample(_ext.desc(logits), _ext.desc(draft), _ext.desc(parent), _ext.desc(pos),
+                                        int(max_hops), float(temperature), float(top_p), int(top_k),
+                                        int(seed) & 0xFFFFFFFFFFFFFFFF, _ext.desc(path), _ext.desc(tokens),
+                                        _ext.desc(info), _ext.desc(nxt), ws.data_ptr(), ws.numel(),
+                                        _ext.stream_of(dev))
+    else:
+        mode_id = {"greedy": _ext.ACCEPT_GREEDY, "typical": _ext.ACCEPT_TYPICAL}[mode]
+        rc = lib.dsv_tree_accept(mode_id, _ext.desc(logits), _ext.desc(draft), _ext.desc(parent), _ext.desc(pos),
+                                 int(max_hops), float(temperature), float(posterior_threshold),
+                                 float(posterior_alpha), _ext.desc(path), _ext.desc(tokens), _ext.desc(info),
+                                 _ext.desc(nxt), ws.data_ptr(), ws.numel(), _ext.stream_of(dev))
     _ext.check(rc, "tree_accept")
     out = {"path": path, "tokens": tokens, "info": info}
     if return_next:
@@ -170,13 +240,13 @@ def _kv_commit_ok(t: torch.Tensor, M: int) -> bool:
 
 
 def _evaluate_tree_dev(logits, draft, parent, position_ids, max_depth, mode, temperature, posterior_threshold,
-                       posterior_alpha):
+                       posterior_alpha, top_p=1.0, top_k=0, seed=0):
     M = draft.shape[-1]
     pos = position_ids[0] if position_ids.dim() == 2 else position_ids
     max_hops = min(int(max_depth) + 2, M)
     r = tree_accept(logits.reshape(1, M, -1), draft.reshape(1, M), parent.reshape(1, M - 1), pos, max_hops,
                     mode=mode, temperature=temperature, posterior_threshold=posterior_threshold,
-                    posterior_alpha=posterior_alpha)
+                    posterior_alpha=posterior_alpha, top_p=top_p, top_k=top_k, seed=seed)
     host = torch.cat([r["info"], r["path"], r["tokens"]], dim=1).cpu()[0].tolist()
     winner, accept_length, _, plen = host[:4]
     if plen < 0:
@@ -212,21 +282,27 @@ def verify(input_ids, logits, draft, position_ids, hidden_states, tree_attention
 def verify_new(input_ids, logits, draft, position_ids, hidden_states, tree_attention_mask, past_key_values_data,
                current_length_data, parent, model, nodes, threshold, max_depth, logits_processor,
                hazard_tracker=None, acceptance: str = "greedy", temperature: float = 1.0,
-               posterior_threshold: float = 0.09, posterior_alpha: float = 0.3):
+               posterior_threshold: float = 0.09, posterior_alpha: float = 0.3, sample_seed: Optional[int] = None):
     """Verify the draft tree and advance the generation state (reference :76-257).
+
+    With ``logits_processor`` (this module's ``prepare_logits_processor`` or
+    the reference's transformers warper list) the draw per node is sampled
+    (mode "sample"); its seed is ``sample_seed`` or, by default, one draw from
+    torch's default generator.
 
     Returns (input_ids, best_candidate, accept_length, next_draft,
     next_position_ids, next_tree_attention_mask, next_parent).
     """
+    top_p, top_k, seed = 1.0, 0, 0
     if logits_processor is not None:
-        raise NotImplementedError(
-            "sampling verification (logits_processor) is not implemented by the MI355X kernels; "
-            "use acceptance='greedy' or acceptance='typical'")
+        sp = _sampling_params(logits_processor)
+        acceptance, temperature, top_p, top_k = "sample", sp.temperature, sp.top_p, sp.top_k
+        seed = int(sample_seed) if sample_seed is not None else int(torch.randint(0, 2 ** 62, (1,)).item())
 
     # 1-2. Acceptance walk on the GPU (reference :100-182).
     (best_candidate, best_candidate_id, accept_length, next_token, max_id), acc = _evaluate_tree_dev(
         logits, draft, parent, position_ids, max_depth, acceptance, temperature, posterior_threshold,
-        posterior_alpha)
+        posterior_alpha, top_p, top_k, seed)
     next_token = next_token.to(draft.device)
     pos_all = position_ids[0] if position_ids.dim() == 2 else position_ids
 

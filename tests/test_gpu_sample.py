@@ -1,0 +1,136 @@
+"""GPU parity of the sampling acceptance (dsv_tree_accept_sample) against the
+oracle (oracle/sampling.py): per-node draws, accepted path, tokens, accept
+length and next token bit-exact; the draws' frequencies against the warped
+softmax by a chi-square test; verify_new driven by the reference's own
+transformers warper list."""
+
+import numpy as np
+import pytest
+import torch
+from scipy import stats
+
+from oracle import sampling as sp
+from diffspec_mi355x import workloads as wl
+from diffspec_mi355x.draft.tree_verification import prepare_logits_processor, tree_accept, verify_new
+
+pytestmark = pytest.mark.gpu
+
+DT = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}
+
+
+def run_and_compare(logits, draft, parent_ref, pos, max_depth, temperature, top_p, top_k, seed):
+    T, M = draft.shape
+    r = tree_accept(logits, draft, parent_ref, pos, min(max_depth + 2, M), mode="sample", temperature=temperature,
+                    top_p=top_p, top_k=top_k, seed=seed, return_next=True)
+    info, path, toks, nxt = (r[k].cpu().numpy() for k in ("info", "path", "tokens", "next"))
+    lg = logits.float().cpu().numpy()
+    for t in range(T):
+        p = pos[t] if pos.dim() == 2 else pos
+        w_toks, w_ids, w_alen, w_next, w_id, draws = sp.sample_walk(
+            lg[t], DT[logits.dtype], draft[t].cpu().numpy(), parent_ref[t].cpu().tolist(), p.cpu().numpy(),
+            max_depth, temperature, top_p, top_k, seed, tree=t)
+        assert nxt[t].tolist() == draws.tolist(), f"tree {t} draws"
+        L = len(w_ids)
+        assert info[t].tolist() == [w_id, w_alen, w_next, L], f"tree {t}"
+        assert path[t, :L].tolist() == w_ids and toks[t, :L].tolist() == w_toks
+    return r
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("temperature,top_p,top_k", [(1.0, 1.0, 0), (0.7, 0.9, 0), (1.3, 1.0, 20), (0.8, 0.5, 10),
+                                                     (1.0, 0.05, 0), (1.0, 1.0, 1)])
+def test_sample_walk_bit_exact(gpu, dtype, temperature, top_p, top_k):
+    print(f"[sample] {dtype} T={temperature} top_p={top_p} top_k={top_k}", flush=True)
+    a = wl.make_accept_inputs(T=2, M=16, V=3000 + 5, dtype=dtype, sigma=2.0, device=str(gpu), seed=11)
+    run_and_compare(a.logits, a.draft, a.parent_ref, a.pos, 8, temperature, top_p, top_k, seed=12345)
+
+
+def test_sample_full_vocab_64_nodes(gpu):
+    """bf16 [1, 64, 128256] N(0, 3) logits, temperature 0.7, top-p 0.9, top-k 50."""
+    a = wl.make_accept_inputs(T=1, M=64, V=128256, device=str(gpu), seed=21)
+    run_and_compare(a.logits, a.draft, a.parent_ref, a.pos, 8, 0.7, 0.9, 50, seed=2 ** 63 + 5)
+    run_and_compare(a.logits, a.draft, a.parent_ref, a.pos, 8, 1.0, 1.0, 0, seed=7)
+
+
+def test_sample_ties_at_the_top_p_cut(gpu):
+    """bf16 rows of a few repeated values, so the top-p cut falls inside a tie
+    group (kept: its highest indices) and top-k ties are all kept."""
+    M, V = 8, 4099
+    g = torch.Generator().manual_seed(5)
+    lg = torch.randint(-3, 3, (1, M, V), generator=g).float().to(torch.bfloat16)
+    lg[0, 3] = float("-inf")
+    lg[0, 3, 17] = 2.0                              # one finite logit
+    lg[0, 4, :] = float("-inf")                     # none: token 0
+    lg[0, 5, 100:200] = float("nan")                # NaN counts as -inf
+    draft = torch.randint(0, V, (1, M), generator=g)
+    parent_ref = torch.tensor([[-1, 0, 1, 2, 3, 4, 5]])
+    pos = torch.arange(M)
+    for top_p, top_k in [(0.3, 0), (0.77, 0), (0.5, 7), (1.0, 3)]:
+        run_and_compare(lg.to(gpu), draft.to(gpu), parent_ref.to(gpu), pos.to(gpu), 8, 1.0, top_p, top_k, seed=99)
+    r = tree_accept(lg.to(gpu), draft.to(gpu), parent_ref.to(gpu), pos.to(gpu), 8, mode="sample", top_p=0.9, seed=4,
+                    return_next=True)
+    assert r["next"][0, 3].item() == 17 and r["next"][0, 4].item() == 0
+
+
+@pytest.mark.parametrize("temperature,top_p,top_k", [(1.0, 1.0, 0), (0.6, 0.85, 0), (1.5, 1.0, 6)])
+def test_sample_frequencies_follow_the_warped_softmax(gpu, temperature, top_p, top_k):
+    """4096 draws of one 24-token row (512 trees x 8 nodes with the same logits)."""
+    V, T, M = 24, 512, 8
+    g = torch.Generator().manual_seed(3)
+    row = torch.randn(V, generator=g) * 1.5
+    lg = row.expand(T, M, V).contiguous().to(gpu)
+    draft = torch.zeros((T, M), dtype=torch.int64, device=gpu)
+    parent_ref = torch.full((T, M - 1), -1, dtype=torch.int64, device=gpu)
+    pos = torch.arange(M, device=gpu)
+    r = tree_accept(lg, draft, parent_ref, pos, 4, mode="sample", temperature=temperature, top_p=top_p, top_k=top_k,
+                    seed=2024, return_next=True)
+    draws = r["next"].reshape(-1).cpu().numpy()
+    y = sp.warp_temperature(row.numpy(), temperature, "f32")
+    keep = sp.kept_mask(y, top_p, top_k)
+    p = np.where(keep, np.exp(y - y.max()), 0.0)
+    p /= p.sum()
+    counts = np.bincount(draws, minlength=V)
+    assert counts[~keep].sum() == 0
+    kept = np.nonzero(keep)[0]
+    assert stats.chisquare(counts[kept], draws.size * p[kept]).pvalue > 1e-4
+    # and bit-exact with the oracle on a few of those trees
+    for t in (0, 1, 511):
+        want = [sp.sample_row(row.numpy(), "f32", temperature, top_p, top_k, 2024, t, i) for i in range(M)]
+        assert r["next"][t].cpu().tolist() == want
+
+
+class _Draft:
+    def __init__(self, dev):
+        self.dev, self.enable_bundle_scheduling = dev, False
+
+    def build_speculative_tree(self, hidden, input_ids, head, nodes, threshold, max_depth):
+        return (torch.tensor([[5, 6]], device=self.dev), torch.tensor([1, 2], device=self.dev),
+                torch.tensor([[1, 0], [1, 1]], device=self.dev), torch.tensor([-1, 0], device=self.dev))
+
+
+class _Model:
+    def __init__(self, dev):
+        self.draft_model = _Draft(dev)
+        self.base_model = type("B", (), {"lm_head": None})()
+
+
+def test_verify_new_with_the_reference_warper_list(gpu):
+    """verify_new given transformers' processor list (what the reference's
+    prepare_logits_processor builds) samples with a seed drawn from torch's
+    default generator: torch.manual_seed fixes the result."""
+    from transformers.generation.logits_process import (LogitsProcessorList, TemperatureLogitsWarper,
+                                                        TopKLogitsWarper, TopPLogitsWarper)
+    a = wl.make_accept_inputs(T=1, M=16, V=2000, sigma=1.0, device=str(gpu), seed=4, pos_offset=30)
+    procs = LogitsProcessorList([TemperatureLogitsWarper(0.8), TopPLogitsWarper(0.9), TopKLogitsWarper(40)])
+    L = 60
+    kv = [torch.randn(2, 1, 2, L, 8, device=gpu)]
+    for lp in (procs, prepare_logits_processor(temperature=0.8, top_p=0.9, top_k=40)):
+        torch.manual_seed(77)
+        seed = int(torch.randint(0, 2 ** 62, (1,)).item())
+        torch.manual_seed(77)
+        res = verify_new(torch.arange(5, device=gpu).unsqueeze(0), a.logits, a.draft, a.pos,
+                         torch.randn(1, 16, 4, device=gpu), None, kv, torch.tensor([L - 4]), a.parent_ref[0],
+                         _Model(gpu), nodes=3, threshold=0.1, max_depth=8, logits_processor=lp)
+        w = sp.sample_walk(a.logits[0].float().cpu().numpy(), "bf16", a.draft[0].cpu().numpy(),
+                           a.parent_ref[0].tolist(), a.pos[0].cpu().numpy(), 8, 0.8, 0.9, 40, seed)
+        assert res[1] == w[0] and res[2] == w[2] and res[3][0, 0].item() == w[3]
