@@ -48,6 +48,9 @@ constexpr float kNegInf = -__builtin_huge_valf();
 // Lazy-rescale threshold in log2 units: the running max used for the
 // exponentials may lag the true max by up to this much (p <= 2^8).
 constexpr float kRescaleTau = 8.0f;
+// Tiles after the first skip their maximum unless a lane's probabilities sum
+// above 2^kSumTau: every probability then stays below 2^kSumTau.
+constexpr float kSumBound = 65536.0f;  // 2^kSumTau, kSumTau = 16
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
@@ -548,36 +551,55 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
       read_k(IC<(S + 1) & 3>{}, kf);
 
       // ---- Y_k: online softmax of S(k) (log2 domain, lazy rescale) ----------
-      if (is_tree || DMASK || k >= nvis) mask_scores(s_cur, k);
-      const float mt = xor32_max(max16(s_cur)) * scale_log2;
-      if (__ballot(mt > mx + kRescaleTau) != 0ull) {
-        const float mn = __builtin_elementwise_maximum(mx, mt);
-        const float al = (mn == mx) ? 1.f : __builtin_amdgcn_exp2f(mx - mn);
-        mx = mn;
-        lsum *= al;
+      // The exponentials run against the lagging row maximum mx.  The tile's
+      // own maximum is taken only where mx is not known yet or the tile is
+      // masked; on other tiles a score above mx + kSumTau shows as a lane's
+      // sum of this tile's probabilities above 2^kSumTau (inf included), and
+      // only then is the tile redone against its maximum.
+      const bool masked = is_tree || DMASK || k >= nvis;
+      if (masked) mask_scores(s_cur, k);
+      auto rescale = [&]() {
+        const float mt = xor32_max(max16(s_cur)) * scale_log2;
+        if (__ballot(mt > mx + kRescaleTau) != 0ull) {
+          const float mn = __builtin_elementwise_maximum(mx, mt);
+          const float al = (mn == mx) ? 1.f : __builtin_amdgcn_exp2f(mx - mn);
+          mx = mn;
+          lsum *= al;
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt) acc[dt] *= al;
-      }
-      const float ms = (mx == kNegInf) ? 0.f : mx;
-      float ls = lsum;
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        __builtin_amdgcn_sched_barrier(0);
-        read_vh(IC<S>{}, hh, vf);
-        __builtin_amdgcn_sched_barrier(0);
-        uint32_t w4[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float p0 = __builtin_amdgcn_exp2f(fmaf(s_cur[hh * 8 + 2 * e], scale_log2, -ms));
-          const float p1 = __builtin_amdgcn_exp2f(fmaf(s_cur[hh * 8 + 2 * e + 1], scale_log2, -ms));
-          w4[e] = pack2<T>(p0, p1);
-          // The normaliser sums the unrounded probabilities: the LSE is an
-          // output in its own right and keeps fp32 accuracy.
-          ls += p0 + p1;
+          for (int dt = 0; dt < DT; ++dt) acc[dt] *= al;
         }
-        pk[hh] = u32x4{w4[0], w4[1], w4[2], w4[3]};
+      };
+      if (masked || __ballot(mx == kNegInf) != 0ull) rescale();
+      auto exps = [&](bool with_v) {
+        const float ms = (mx == kNegInf) ? 0.f : mx;
+        float ts = 0.f;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          if (with_v) {
+            __builtin_amdgcn_sched_barrier(0);
+            read_vh(IC<S>{}, hh, vf);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+          uint32_t w4[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float p0 = __builtin_amdgcn_exp2f(fmaf(s_cur[hh * 8 + 2 * e], scale_log2, -ms));
+            const float p1 = __builtin_amdgcn_exp2f(fmaf(s_cur[hh * 8 + 2 * e + 1], scale_log2, -ms));
+            w4[e] = pack2<T>(p0, p1);
+            // The normaliser sums the unrounded probabilities: the LSE is an
+            // output in its own right and keeps fp32 accuracy.
+            ts += p0 + p1;
+          }
+          pk[hh] = u32x4{w4[0], w4[1], w4[2], w4[3]};
+        }
+        return ts;
+      };
+      float ts = exps(true);
+      if (!masked && __ballot(!(ts <= kSumBound)) != 0ull) {
+        rescale();
+        ts = exps(false);
       }
-      lsum = ls;
+      lsum += ts;
     }
     if (v_wave) sync(IC<(S + 3) & 3>{}, k);
     if (wave_active) {
