@@ -406,9 +406,12 @@ def bench_accept(args, lib, ev):
     T, M, V = 8, 64, 128256
     a = wl.make_accept_inputs(T=T, M=M, V=V, device="cuda", pos_offset=65536)
     res = {}
-    for mode in ("greedy", "typical"):
+    kws = {"greedy": {}, "typical": {}, "sample": dict(temperature=0.7, top_p=0.9, top_k=50, seed=1234),
+           "sample_temperature_only": dict(temperature=0.7, seed=1234)}
+    for name, kw in kws.items():
+        mode = "sample" if name.startswith("sample") else name
         for _ in range(3):
-            tree_accept(a.logits, a.draft, a.parent_ref, a.pos, 10, mode=mode)
+            tree_accept(a.logits, a.draft, a.parent_ref, a.pos, 10, mode=mode, **kw)
         torch.cuda.synchronize()
         n = 20
         evs = ev.create(2 * n)
@@ -416,7 +419,7 @@ def bench_accept(args, lib, ev):
         e0.record()
         for i in range(n):
             lib.dsv_set_timing_events(evs[2 * i], evs[2 * i + 1])
-            r = tree_accept(a.logits, a.draft, a.parent_ref, a.pos, 10, mode=mode)
+            r = tree_accept(a.logits, a.draft, a.parent_ref, a.pos, 10, mode=mode, **kw)
         e1.record()
         torch.cuda.synchronize()
         sweep = statistics.median(ev.elapsed_ms(evs[2 * i], evs[2 * i + 1]) for i in range(n))
@@ -426,7 +429,7 @@ def bench_accept(args, lib, ev):
         # replayed n times (the acceptance path records no memset nodes).
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            rg = tree_accept(a.logits, a.draft, a.parent_ref, a.pos, 10, mode=mode)
+            rg = tree_accept(a.logits, a.draft, a.parent_ref, a.pos, 10, mode=mode, **kw)
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(rg["info"], r["info"]), "graph replay differs from the eager call"
@@ -437,8 +440,10 @@ def bench_accept(args, lib, ev):
         e3.record()
         torch.cuda.synchronize()
         assert torch.equal(rg["info"], r["info"]), "graph replay differs from the eager call"
-        res[mode] = {"us_total": e2.elapsed_time(e3) / n * 1e3, "us_total_eager": e0.elapsed_time(e1) / n * 1e3,
+        res[name] = {"us_total": e2.elapsed_time(e3) / n * 1e3, "us_total_eager": e0.elapsed_time(e1) / n * 1e3,
                      "us_vocab_sweep": sweep * 1e3, "accept_lengths": r["info"][:, 1].tolist()}
+        if mode == "sample":
+            res[name]["params"] = {k: v for k, v in kw.items() if k != "seed"}
     nbytes = T * M * V * 2
     for mode in res:
         res[mode]["sweep_gbs"] = nbytes / (res[mode]["us_vocab_sweep"] * 1e-6) / 1e9
@@ -450,8 +455,10 @@ def cpu_baseline(inp, args):
     from oracle import ref_cpu_path as rc
     from oracle import attention as oa
 
-    cores = len(os.sched_getaffinity(0))
-    cores = min(cores, int(os.environ.get("BENCH_CPU_THREADS", "16")))
+    # Every core of the affinity mask, unless the box caps this process's CPU
+    # share through OMP_NUM_THREADS (the GPU boxes give one GPU 16 threads).
+    affinity = len(os.sched_getaffinity(0))
+    cores = min(affinity, int(os.environ.get("OMP_NUM_THREADS", affinity)))
     torch.set_num_threads(cores)
     n_prefix, M = inp.n_prefix, inp.M
     k = inp.logical_kv(0, 0)[0].float().cpu().transpose(0, 1).unsqueeze(0).contiguous()  # [1, Hk, L, D]
@@ -466,7 +473,8 @@ def cpu_baseline(inp, args):
         times.append(time.perf_counter() - t0)
         if len(times) >= args.cpu_max_steps:
             break
-    return {"value": statistics.median(times) * 1e6, "unit": "us/verify-step", "cores": cores, "kind": "port",
+    return {"value": statistics.median(times) * 1e6, "unit": "us/verify-step", "cores": cores,
+            "affinity_cores": affinity, "threads": torch.get_num_threads(), "kind": "port",
             "sample": f"{len(times)} full verify steps (1 layer, N={n_prefix}, M={M}, fp32 upcast), "
                       f"median"}, out
 
@@ -542,6 +550,9 @@ def main():
         "roofline": {"kernel": "attn_splitk_kernel (kernel 1: prefix splits + tree split)", "bound": "hbm",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "traffic_source": "profiles/attn_splitk_64k_traffic.json: rocprofv3 FETCH_SIZE and WRITE_SIZE "
+                                       "per dispatch of this kernel on this workload (two counter passes), scaled "
+                                       "by a 1 GiB copy; re-measured whenever kernel 1 changes",
                      "bytes_per_launch": nb["kernel1"], "avg_us": round(k1_us, 3), "median_us": round(k1_med, 3),
                      "timing": "HIP start/stop events attached to each kernel-1 launch (hipExtLaunchKernel), "
                                "second pass of K steps", "us_per_step_in_that_pass": round(ms_step_ev * 1e3, 3)},

@@ -48,6 +48,9 @@ uintptr_t elem_addr(const void* base, int64_t elem, int esize) {
   return (uintptr_t)base + (uintptr_t)(elem * esize);
 }
 
+// Highest LDS byte address (exclusive) an LDS-DMA destination may reach.
+constexpr int kLdsDmaLimit = 65536;
+
 template <int D>
 void check_kernel1(const AttnArgs& a, bool dmask, const AttnExtents& ex, Checker& ck) {
   using G = Geo<D>;
@@ -106,6 +109,10 @@ void check_kernel1(const AttnArgs& a, bool dmask, const AttnExtents& ex, Checker
             dma_ins<D>(i, is_v, j);
             const int dst = (stage * 2 + (is_v ? 1 : 0)) * G::TILE + j * 1024;
             ck.cond(dst >= 0 && dst + 1024 <= RING, "LDS-DMA destination outside the ring");
+            // Lane l of an LDS-DMA instruction writes 16 bytes at M0 + 16 l:
+            // every such destination stays below 64 KiB.
+            for (int l = 0; l < 64; ++l)
+              ck.cond(dst + 16 * l + 16 <= kLdsDmaLimit, "LDS-DMA lane destination at or above 64 KiB");
             const uint16_t* base = is_v ? src.v : src.k;
             const Extent& e = is_v ? ev : ek;
             for (int lane = 0; lane < 64 && ck.ok; ++lane) {

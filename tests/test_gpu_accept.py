@@ -269,3 +269,55 @@ def test_verify_new_takes_the_reference_copy_beyond_the_commit_kernel_limit(gpu)
     sel = torch.tensor(w[1], device=gpu) + start
     for x, x0 in zip(kv, kv_before):
         assert torch.equal(x[..., start:start + len(w[1]), :], x0[..., sel, :])
+
+
+def _near_threshold_rows(n, V, delta, sigma, rng, temperature=1.0, eps=0.09, alpha=0.3):
+    """fp32 rows whose token 0 has p = (1 + delta) * min(eps, alpha * exp(-H)) under
+    softmax(row / T): the logit of token 0 is solved by bisection in float64
+    (the distance is checked after rounding it to float32)."""
+    rows, got = [], []
+    for _ in range(n):
+        x = rng.normal(0, sigma, V).astype(np.float64)
+
+        def f(v):
+            x[0] = v
+            p, ent = oacc.softmax_stats(x.astype(np.float32), temperature)
+            return np.log(p[0]) - np.log(min(eps, alpha * np.exp(-ent))) - np.log1p(delta)
+
+        lo, hi = -30.0 * temperature, 30.0 * temperature
+        if f(lo) * f(hi) > 0:
+            continue
+        for _ in range(200):
+            mid = 0.5 * (lo + hi)
+            if (f(mid) > 0) == (f(hi) > 0):
+                hi = mid
+            else:
+                lo = mid
+        x[0] = np.float32(hi if f(hi) * np.sign(delta) > 0 else lo)
+        p, ent = oacc.softmax_stats(x.astype(np.float32), temperature)
+        ratio = p[0] / min(eps, alpha * np.exp(-ent))
+        if np.sign(ratio - 1.0) == np.sign(delta) and abs(ratio - 1.0) >= abs(delta) * 0.5:
+            rows.append(x.astype(np.float32))
+            got.append(ratio)
+    return np.stack(rows), np.array(got)
+
+
+@pytest.mark.parametrize("delta", [2e-3, -2e-3, 5e-4, -5e-4])
+@pytest.mark.parametrize("sigma", [0.5, 3.0])
+def test_typical_decision_near_the_threshold(gpu, delta, sigma):
+    """The typical test p > min(eps, alpha * exp(-H)) is decided from fp32
+    statistics of the vocabulary sweep (hardware exp2, fp32 sums): it agrees
+    with the fp64 oracle whenever the draft token's probability is more than
+    2.5e-4 (relative) away from the threshold.  sigma 0.5 gives flat rows
+    (threshold alpha * exp(-H)), sigma 3 peaked ones (threshold eps for many)."""
+    rng = np.random.default_rng(int(abs(delta) * 1e6) + int(sigma * 10) + (delta > 0))
+    rows, ratio = _near_threshold_rows(48, 20000, delta, sigma, rng, temperature=0.9)
+    T = rows.shape[0]
+    assert T >= 24
+    lg = torch.from_numpy(np.stack([rows, rows], axis=1))        # [T, 2, V]: root and its child
+    draft = torch.zeros((T, 2), dtype=torch.int64)                  # the child's token is token 0
+    parent_ref = torch.full((T, 1), -1, dtype=torch.int64)
+    pos = torch.tensor([0, 1])
+    kw = dict(temperature=0.9, posterior_threshold=0.09, posterior_alpha=0.3)
+    info = run_and_compare(lg.to(gpu), draft.to(gpu), parent_ref.to(gpu), pos.to(gpu), 8, mode="typical", **kw)
+    assert (info[:, 1] == (1 if delta > 0 else 0)).all()
