@@ -30,9 +30,9 @@ Definitions (per node row x of the logits, vocabulary V):
   top-k    (k > 0) keep v iff y_v >= the k-th largest y (with multiplicity),
            applied after top-p, which is the same as intersecting with the
            top-k set of the unfiltered row (TopKLogitsWarper)
-  U_v      Philox4x64-10 (Salmon et al. 2011; numpy.random.Philox) with key
-           (seed, 0) and counter (v, node, tree, 0): word 0 w gives
-           U = ((w >> 12) + 0.5) * 2^-52 in (0, 1)
+  U_v      Philox4x32-10 (Salmon et al. 2011, the Random123 generator) with
+           key (seed mod 2^32, seed >> 32) and counter (v >> 2, node, tree, 0):
+           output word v & 3, w, gives U = (w + 0.5) * 2^-32 in (0, 1)
   G_v      -det_ln(-det_ln(U_v))
   token    argmax over kept v of y_v + G_v (double), lowest index on ties;
            0 when nothing is kept (a row without a finite logit)
@@ -50,8 +50,9 @@ from .attention import bf16_round, half_round
 U64 = np.uint64
 MASK32 = U64(0xFFFFFFFF)
 
-PHILOX_M0, PHILOX_M1 = 0xD2E7470EE14C6C93, 0xCA5A826395121157
-PHILOX_W0, PHILOX_W1 = 0x9E3779B97F4A7C15, 0xBB67AE8584CAA73B
+PHILOX_M0, PHILOX_M1 = 0xD2511F53, 0xCD9E8D57
+PHILOX_W0, PHILOX_W1 = 0x9E3779B9, 0xBB67AE85
+
 
 # ln(2)^k / k!, k = 0..17, and 1 / (2k + 1), k = 0..11, as correctly rounded doubles.
 EXP2_C = [float.fromhex(h) for h in (
@@ -73,38 +74,29 @@ SQRT_HALF = float.fromhex("0x1.6a09e667f3bcdp-1")
 # Counter-based uniforms
 # ----------------------------------------------------------------------------
 
-def _mul64(a: np.ndarray, b: int) -> Tuple[np.ndarray, np.ndarray]:
-    """Full 128-bit product of uint64 arrays a and a 64-bit constant b: (hi, lo)."""
-    a = a.astype(U64)
-    a_lo, a_hi = a & MASK32, a >> U64(32)
-    b_lo, b_hi = U64(b & 0xFFFFFFFF), U64(b >> 32)
-    ll, hl, lh, hh = a_lo * b_lo, a_hi * b_lo, a_lo * b_hi, a_hi * b_hi
-    cross = (ll >> U64(32)) + (hl & MASK32) + (lh & MASK32)
-    lo = (ll & MASK32) | ((cross & MASK32) << U64(32))
-    hi = hh + (hl >> U64(32)) + (lh >> U64(32)) + (cross >> U64(32))
-    return hi, lo
-
-
-def philox4x64_10(c0, c1, c2, c3, k0: int, k1: int):
-    """Philox4x64 with 10 rounds on uint64 arrays (counter words c0..c3, key k0, k1)."""
-    c = [np.asarray(x, dtype=U64) for x in (c0, c1, c2, c3)]
+def philox4x32_10(c0, c1, c2, c3, k0: int, k1: int):
+    """Philox4x32 with 10 rounds on arrays of 32-bit counter words (held in
+    uint64), key (k0, k1): the four output words."""
+    c = [np.asarray(x, dtype=U64) & MASK32 for x in (c0, c1, c2, c3)]
     c = list(np.broadcast_arrays(*c))
-    k0, k1 = U64(k0 & 0xFFFFFFFFFFFFFFFF), U64(k1 & 0xFFFFFFFFFFFFFFFF)
-    with np.errstate(over="ignore"):
-        for r in range(10):
-            if r:
-                k0 = U64((int(k0) + PHILOX_W0) & 0xFFFFFFFFFFFFFFFF)
-                k1 = U64((int(k1) + PHILOX_W1) & 0xFFFFFFFFFFFFFFFF)
-            hi0, lo0 = _mul64(c[0], PHILOX_M0)
-            hi1, lo1 = _mul64(c[2], PHILOX_M1)
-            c = [hi1 ^ c[1] ^ k0, lo1, hi0 ^ c[3] ^ k1, lo0]
+    k0, k1 = int(k0) & 0xFFFFFFFF, int(k1) & 0xFFFFFFFF
+    for r in range(10):
+        if r:
+            k0 = (k0 + PHILOX_W0) & 0xFFFFFFFF
+            k1 = (k1 + PHILOX_W1) & 0xFFFFFFFF
+        p0 = c[0] * U64(PHILOX_M0)          # < 2^64: exact in uint64
+        p1 = c[2] * U64(PHILOX_M1)
+        c = [(p1 >> U64(32)) ^ c[1] ^ U64(k0), p1 & MASK32, (p0 >> U64(32)) ^ c[3] ^ U64(k1), p0 & MASK32]
     return c
 
 
 def uniforms(seed: int, tree: int, node: int, V: int) -> np.ndarray:
     """U_v in (0, 1) for v in [0, V) of one node."""
-    w = philox4x64_10(np.arange(V, dtype=U64), U64(node), U64(tree), U64(0), seed, 0)[0]
-    return ((w >> U64(12)).astype(np.float64) + 0.5) * 2.0 ** -52
+    v = np.arange(V, dtype=U64)
+    seed = int(seed) & 0xFFFFFFFFFFFFFFFF
+    words = np.stack(philox4x32_10(v >> U64(2), U64(node), U64(tree), U64(0), seed & 0xFFFFFFFF, seed >> 32))
+    w = words[(v & U64(3)).astype(np.int64), np.arange(V)]
+    return (w.astype(np.float64) + 0.5) * 2.0 ** -32
 
 
 # ----------------------------------------------------------------------------

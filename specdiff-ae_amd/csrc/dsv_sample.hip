@@ -12,20 +12,34 @@
 //   top-p: keep v iff the mass ranked above v < Tq = ceil(P * L / 2^32),
 //   L = sum q, P = rint(top_p * 2^32).  top-k: keep y >= the k-th largest y.
 //   Draw: argmax over kept v of y_v + G_v (double, lowest index on ties),
-//   G_v = -ln(-ln U_v), U_v from Philox4x64-10 (Salmon et al. 2011) with key
-//   (seed, 0) and counter (v, node, tree, 0): a Gumbel-max draw from
-//   softmax(y) over the kept set.
+//   G_v = -ln(-ln U_v), U_v = (w + 0.5) 2^-32 with w the output word v & 3 of
+//   Philox4x32-10 (Salmon et al. 2011) at key (seed mod 2^32, seed >> 32) and
+//   counter (v >> 2, node, tree, 0): a Gumbel-max draw from softmax(y) over
+//   the kept set, one generator call per four vocabulary entries.
 // The logarithms and 2^x are evaluated with a fixed sequence of double
 // operations (no fused multiply-add, no library call), each correctly
 // rounded, so the draws are reproducible bit for bit off the GPU.
 //
 // Kernels:
-//   sample_select_kernel  one workgroup per row, only with top-p or top-k:
-//       8-bit radix selection over the order keys of y (count-weighted for
-//       top-k, mass-weighted for top-p), then over the indices of the tie
-//       group at the top-p cut; writes the kept-set bounds of the row.
-//   sample_sweep_kernel   one workgroup per (row, vocabulary range): the
-//       Gumbel-max draw over the range's kept entries.
+//   sample_select_kernel  one workgroup per row, only with top-p or top-k.
+//       Fast path: the row maximum m, then counts of y >= m - theta_j for a
+//       ladder of thetas (wave ballots), then the candidates y >= m - theta*
+//       (at most kCap, a head of the order) are gathered into LDS and sorted.
+//       top-k is the candidates' k-th key; top-p takes the exact masses of
+//       the candidates and bounds the rest of L by an fp32 sum (relative
+//       error far below the 2^-12 allowed): the cut is exact whenever it lies
+//       inside the candidates for every L in those bounds.  The draw is then
+//       taken over the kept candidates and written as the row's result.
+//       Otherwise (a flat row, a large k, an undecided cut): 8-bit radix
+//       selection over the order keys of y (count-weighted for top-k,
+//       mass-weighted for top-p), then over the indices of the tie group at
+//       the top-p cut; the kept-set bounds go to the sweep.
+//   sample_sweep_kernel   one workgroup per (row, vocabulary range) of the
+//       rows the select kernel left open (all rows without top-p / top-k):
+//       the Gumbel-max draw over the range's kept entries.  An fp32 estimate
+//       of each z (within 2^-14 of it) against a wave-shared lower bound of
+//       the range's maximum z leaves the exact double evaluation to the few
+//       entries that can still win.
 //   the walk of dsv_accept.hip combines the ranges' draws and walks.
 
 #include "dsv_internal.h"
@@ -37,6 +51,20 @@ namespace {
 constexpr int kSelThreads = 1024;
 constexpr int kSweepThreads = 256;
 constexpr float kNegInfF = -__builtin_huge_valf();
+constexpr int kCap = 4096;   // candidates the select kernel's fast path sorts in LDS
+static_assert(kCap % kSelThreads == 0, "candidates split evenly over the threads");
+// Ladder of candidate thresholds m - y <= theta_j: the floats whose bits are
+// (250 + j) << 22, i.e. 2^e and 1.5 * 2^e from 1/4 to 48.
+constexpr int kNTheta = 16;
+__constant__ float kTheta[kNTheta] = {0.25f, 0.375f, 0.5f, 0.75f, 1.f, 1.5f, 2.f, 3.f,
+                                      4.f,   6.f,    8.f,  12.f,  16.f, 24.f, 32.f, 48.f};
+// Upper bound of the fp32 Gumbel estimate: U <= 1 - 2^-33 gives G < 22.9.
+constexpr float kGumbelMax = 23.f;
+// Margin of the fp32 estimate of z = y + G: the estimate is within 2^-14 of
+// the double value (hardware log2 to about 1 ulp, fp32 rounding of U, 1 - U,
+// -ln U and the sum); the margin is 2^-7 plus 2^-20 of |z|.
+constexpr float kZMargin = 0x1p-7f;
+constexpr float kZMarginRel = 0x1p-20f;
 
 // ln(2)^k / k!, k = 0..17, and 1 / (2k + 1), k = 0..11 (correctly rounded).
 __constant__ double kExp2C[18] = {
@@ -90,33 +118,58 @@ __device__ __forceinline__ double det_exp2(double u) {
   return __builtin_ldexp(p, (int)n);
 }
 
-// Philox4x64-10, word 0 of the output block.
-__device__ __forceinline__ uint64_t philox_word0(uint64_t c0, uint64_t c1, uint64_t c2, uint64_t c3, uint64_t k0,
-                                                 uint64_t k1) {
-  constexpr uint64_t M0 = 0xD2E7470EE14C6C93ull, M1 = 0xCA5A826395121157ull;
-  constexpr uint64_t W0 = 0x9E3779B97F4A7C15ull, W1 = 0xBB67AE8584CAA73Bull;
+// Philox4x32-10: the four output words of counter (c0, c1, c2, c3), key (k0, k1).
+__device__ __forceinline__ uint4 philox4x32(uint32_t c0, uint32_t c1, uint32_t c2, uint32_t c3, uint32_t k0,
+                                            uint32_t k1) {
+  constexpr uint32_t M0 = 0xD2511F53u, M1 = 0xCD9E8D57u, W0 = 0x9E3779B9u, W1 = 0xBB67AE85u;
 #pragma unroll
   for (int r = 0; r < 10; ++r) {
     if (r) {
       k0 += W0;
       k1 += W1;
     }
-    const uint64_t hi0 = __umul64hi(M0, c0), lo0 = M0 * c0;
-    const uint64_t hi1 = __umul64hi(M1, c2), lo1 = M1 * c2;
-    const uint64_t n0 = hi1 ^ c1 ^ k0, n2 = hi0 ^ c3 ^ k1;
+    // One 32 x 32 -> 64-bit product each (v_mad_u64_u32).
+    const uint64_t p0 = (uint64_t)M0 * c0, p1 = (uint64_t)M1 * c2;
+    const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c1 ^ k0, n2 = (uint32_t)(p0 >> 32) ^ c3 ^ k1;
     c0 = n0;
-    c1 = lo1;
+    c1 = (uint32_t)p1;
     c2 = n2;
-    c3 = lo0;
+    c3 = (uint32_t)p0;
   }
-  return c0;
+  return make_uint4(c0, c1, c2, c3);
 }
 
-// G = -ln(-ln U), U = ((w >> 12) + 0.5) * 2^-52.
-__device__ __forceinline__ double gumbel(uint64_t w) {
+__device__ __forceinline__ uint32_t word_of(const uint4& w, int e) {
+  return e == 0 ? w.x : (e == 1 ? w.y : (e == 2 ? w.z : w.w));
+}
+
+// The draw's random word of vocabulary entry v of row (tree t, node i).
+__device__ __forceinline__ uint32_t draw_word(int64_t v, int i, int t, uint64_t seed) {
+  const uint4 w = philox4x32((uint32_t)(v >> 2), (uint32_t)i, (uint32_t)t, 0u, (uint32_t)seed, (uint32_t)(seed >> 32));
+  return word_of(w, (int)(v & 3));
+}
+
+// G = -ln(-ln U), U = (w + 0.5) * 2^-32, in double (the definition).  Not
+// inlined: the filters leave it to few entries, and one copy keeps the
+// kernels small.
+__device__ __noinline__ double gumbel(uint32_t w) {
 #pragma clang fp contract(off)
-  const double u = ((double)(w >> 12) + 0.5) * 0x1p-52;
+  const double u = ((double)w + 0.5) * 0x1p-32;
   return -det_ln(-det_ln(u));
+}
+
+// fp32 estimate of gumbel(w).  -ln U from U for U < 1/2, else from
+// x = 1 - U = (~w + 0.5) 2^-32 (a series below 2^-7), so that -ln U keeps its
+// relative accuracy as U approaches 1.
+__device__ __forceinline__ float gumbel_est(uint32_t w) {
+  float e;
+  if (w < 0x80000000u) {
+    e = -__logf(((float)w + 0.5f) * 0x1p-32f);
+  } else {
+    const float x = ((float)(~w) + 0.5f) * 0x1p-32f;
+    e = x < 0x1p-7f ? x * (1.f + x * (0.5f + x * (1.f / 3.f))) : -__logf(1.f - x);
+  }
+  return -__logf(e);
 }
 
 template <typename LT>
@@ -134,28 +187,139 @@ __device__ __forceinline__ float raw_to_f<float>(float x) {
   return x;
 }
 
-// y of one logit: x / T rounded to the logits dtype (T == 1: x); NaN -> -inf, -0 -> +0.
-template <typename LT>
-__device__ __forceinline__ float warp_y(LT raw, float T) {
-  float y = raw_to_f<LT>(raw);
-  if (T != 1.f) {
-    y = y / T;  // IEEE division (correctly rounded by default in HIP)
-    if constexpr (sizeof(LT) == 2) {
-      if constexpr (__is_same(LT, _Float16))
-        y = (float)(_Float16)y;
-      else
-        y = (float)(__bf16)y;
-    }
-  }
+// The temperature warper's constants.
+struct Warp {
+  float T, rT;  // T and fl(1 / T)
+};
+__device__ __forceinline__ Warp make_warp(float T) { return Warp{T, 1.f / T}; }
+
+// NaN counts as -inf, -0 as +0.
+__device__ __forceinline__ float clean_y(float y) {
   if (y != y) y = kNegInfF;
   if (y == 0.f) y = 0.f;
   return y;
+}
+
+template <typename LT>
+__device__ __forceinline__ float round_lt(float y) {
+  if constexpr (__is_same(LT, _Float16))
+    return (float)(_Float16)y;
+  else if constexpr (__is_same(LT, uint16_t))
+    return (float)(__bf16)y;
+  else
+    return y;
+}
+
+// y of one logit: x / T (IEEE division, correctly rounded by default in HIP)
+// rounded to the logits dtype (T == 1: x); NaN -> -inf, -0 -> +0.
+template <typename LT>
+__device__ __forceinline__ float warp_y(LT raw, const Warp& w) {
+  float y = raw_to_f<LT>(raw);
+  if (w.T != 1.f) y = round_lt<LT>(y / w.T);
+  return clean_y(y);
+}
+
+// warp_y of N values held as floats.  For 16-bit logits q = x * fl(1/T) lies
+// within 3 fp32 ulp of the correctly rounded quotient; both round to the same
+// 16-bit value unless q is within 8 ulp of a rounding midpoint or outside the
+// dtype's normal range, and only there (for the wave: only when some lane has
+// such an entry) the division decides.
+template <typename LT, int N>
+__device__ __forceinline__ void warp_vec(float (&y)[N], const Warp& w) {
+  if (w.T != 1.f) {
+    if constexpr (sizeof(LT) == 2) {
+      constexpr bool kF16 = __is_same(LT, _Float16);
+      constexpr int LOW = kF16 ? 13 : 16;  // fp32 mantissa bits below the 16-bit type's
+      constexpr uint32_t MID = 1u << (LOW - 1);
+      constexpr float kLo = kF16 ? 0x1p-14f : 0x1p-100f, kHi = kF16 ? 32768.f : 0x1p100f;
+      float q[N];
+      bool unsafe[N], any = false;
+#pragma unroll
+      for (int e = 0; e < N; ++e) {
+        q[e] = y[e] * w.rT;
+        const uint32_t low = __float_as_uint(q[e]) & ((1u << LOW) - 1u);
+        const float aq = fabsf(q[e]);
+        unsafe[e] = !((low > MID + 8u || low + 8u < MID) && aq >= kLo && aq <= kHi);
+        any |= unsafe[e];
+      }
+      if (__ballot(any) != 0ull) {
+#pragma unroll
+        for (int e = 0; e < N; ++e)
+          if (unsafe[e]) q[e] = y[e] / w.T;
+      }
+#pragma unroll
+      for (int e = 0; e < N; ++e) y[e] = round_lt<LT>(q[e]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < N; ++e) y[e] = y[e] / w.T;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < N; ++e) y[e] = clean_y(y[e]);
+}
+
+// The logit of dtype LT whose value is f (f is such a value).
+template <typename LT>
+__device__ __forceinline__ LT f_to_raw(float f) {
+  if constexpr (__is_same(LT, uint16_t))
+    return (uint16_t)(__float_as_uint(f) >> 16);
+  else
+    return (LT)f;
 }
 
 // Order-preserving 32-bit key of y.
 __device__ __forceinline__ uint32_t ykey(float y) {
   const uint32_t b = __float_as_uint(y);
   return b ^ ((b >> 31) ? 0xFFFFFFFFu : 0x80000000u);
+}
+
+// y of N = 16 / sizeof(LT) consecutive logits from v0 (entries at or past hi
+// read as -inf): one 16-byte load when the row is 16-byte aligned.
+template <typename LT, bool WARP>
+__device__ __forceinline__ void load_y(const LT* x, int64_t v0, int64_t hi, bool aligned, const Warp& T,
+                                       float (&y)[16 / sizeof(LT)]) {
+  constexpr int N = 16 / sizeof(LT);
+  if (aligned && v0 + N <= hi) {
+    const u32x4 r = *reinterpret_cast<const u32x4*>(x + v0);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if constexpr (sizeof(LT) == 4) {
+        y[e] = __uint_as_float(r[e]);
+      } else {
+        y[2 * e] = raw_to_f<LT>(__builtin_bit_cast(LT, (uint16_t)(r[e] & 0xFFFFu)));
+        y[2 * e + 1] = raw_to_f<LT>(__builtin_bit_cast(LT, (uint16_t)(r[e] >> 16)));
+      }
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < N; ++e) y[e] = v0 + e < hi ? raw_to_f<LT>(x[v0 + e]) : kNegInfF;
+  }
+  if constexpr (WARP) {
+    warp_vec<LT, N>(y, T);
+  } else {
+#pragma unroll
+    for (int e = 0; e < N; ++e) y[e] = clean_y(y[e]);
+  }
+}
+
+// Runs f(v0, y) over [lo, hi) in vectors of N entries (lo a multiple of N):
+// the threads of a block take consecutive vectors, two vectors per thread and
+// iteration with both loads in flight.  Every lane of a wave runs the same
+// iterations, so f may use wave ballots and shuffles.  WARP = false hands f
+// the logits themselves (NaN as -inf).
+template <typename LT, int NT, bool WARP = true, typename F>
+__device__ __forceinline__ void row_sweep(const LT* x, int64_t lo, int64_t hi, const Warp& T, F&& f) {
+  constexpr int N = 16 / sizeof(LT);
+  const bool aligned = (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+  const int lane = threadIdx.x & 63;
+  for (int64_t b0 = lo + (int64_t)(threadIdx.x & ~63) * N; b0 < hi; b0 += (int64_t)2 * NT * N) {
+    const int64_t v0 = b0 + (int64_t)lane * N, v1 = v0 + (int64_t)NT * N;
+    float ya[N], yb[N];
+    load_y<LT, WARP>(x, v0, hi, aligned, T, ya);
+    load_y<LT, WARP>(x, v1, hi, aligned, T, yb);
+    f(v0, ya);
+    f(v1, yb);
+  }
 }
 
 // Fixed-point mass of y given the row maximum m: rint(2^(S + (y - m) log2 e)).
@@ -182,6 +346,46 @@ constexpr int key_digits() {
 __device__ __forceinline__ uint32_t fill_low(uint32_t prefix, int nd) {
   if (nd >= 4 || (prefix >> 31)) return prefix;
   return prefix | ((1u << (32 - 8 * nd)) - 1u);
+}
+
+// The y of an order key (inverse of ykey).
+__device__ __forceinline__ float key_to_y(uint32_t k) {
+  return __uint_as_float(k ^ ((k >> 31) ? 0x80000000u : 0xFFFFFFFFu));
+}
+
+// Tq = ceil(P * L / 2^32) with a 128-bit product.
+__device__ __forceinline__ uint64_t tq_of(uint64_t P, uint64_t L) {
+  const uint64_t lo = P * L, hi = __umul64hi(P, L);
+  const uint64_t lo2 = lo + 0xFFFFFFFFull;
+  const uint64_t hi2 = hi + (lo2 < lo ? 1ull : 0ull);
+  return (lo2 >> 32) | (hi2 << 32);
+}
+
+// Block argmax of (z, index): larger z, then lower index; -1 = none.  Every
+// thread calls it; thread 0 gets the result.
+__device__ __forceinline__ void block_argmax(double& best, int& bi, double* sb, int* si, int nthreads) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const double ob = __shfl_xor(best, o);
+    const int oi = __shfl_xor(bi, o);
+    if (oi >= 0 && (bi < 0 || ob > best || (ob == best && oi < bi))) {
+      best = ob;
+      bi = oi;
+    }
+  }
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    sb[w] = best;
+    si[w] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int k = 1; k < nthreads / 64; ++k)
+      if (si[k] >= 0 && (bi < 0 || sb[k] > best || (sb[k] == best && si[k] < bi))) {
+        best = sb[k];
+        bi = si[k];
+      }
+  }
 }
 
 // Descending scan of a 256-bin histogram by wave 0: the first bin b (from 255
@@ -228,15 +432,21 @@ __global__ void __launch_bounds__(kSelThreads) sample_select_kernel(const Accept
   const int V = (int)a.V;
   const int tid = threadIdx.x;
   constexpr int ND = key_digits<LT>();
+  const Warp wp = make_warp(a.temperature);
 
   __shared__ uint64_t hist[256];
   __shared__ float red_f[kSelThreads / 64];
   __shared__ uint32_t res_u[4];
   __shared__ uint64_t res_q[4];
 
-  // Row maximum of y.
+  // Row maximum of y: the warper is monotone, so it is the warped maximum
+  // logit (xm).
   float m = kNegInfF;
-  for (int v = tid; v < V; v += kSelThreads) m = fmaxf(m, warp_y<LT>(x[v], a.temperature));
+  constexpr int NV = 16 / sizeof(LT);
+  row_sweep<LT, kSelThreads, false>(x, 0, V, wp, [&](int64_t, const float(&y)[NV]) {
+#pragma unroll
+    for (int e = 0; e < NV; ++e) m = fmaxf(m, y[e]);
+  });
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
   if ((tid & 63) == 0) red_f[tid >> 6] = m;
@@ -247,10 +457,291 @@ __global__ void __launch_bounds__(kSelThreads) sample_select_kernel(const Accept
     red_f[0] = mm;
   }
   __syncthreads();
-  m = red_f[0];
+  const float xm = red_f[0];
+  m = xm > kNegInfF ? warp_y<LT>(f_to_raw<LT>(xm), wp) : kNegInfF;
 
   int S = 63;
   for (int vv = V; vv > 0; vv >>= 1) --S;  // 63 - bitlen(V)
+
+  const int lane = tid & 63, wv = tid >> 6;
+  const int64_t kk = (a.top_k > 0 && a.top_k < V) ? a.top_k : 0;
+  const bool use_p = a.top_p_q != 0;
+  // The row's draw, written by thread 0 as range 0's result (the other
+  // ranges report none); the sweep then skips the row.
+  auto finish = [&](double z, int idx) {
+    const uint64_t zb = __builtin_bit_cast(uint64_t, z);
+    for (int c = 0; c < a.nchunk; ++c)
+      a.rstat[row * a.nchunk + c] =
+          c == 0 ? make_float4(__uint_as_float((uint32_t)zb), __uint_as_float((uint32_t)(zb >> 32)), __int_as_float(idx), 0.f)
+                 : make_float4(0.f, 0.f, __int_as_float(-1), 0.f);
+    a.sel[row] = make_uint4(0u, 0u, 0u, 1u);
+  };
+  if (!(m > kNegInfF)) {  // no finite logit: nothing is kept (token 0)
+    if (tid == 0) finish(0.0, -1);
+    return;
+  }
+  if (!use_p && kk == 0) {  // top-k of at least V: everything is kept
+    if (tid == 0) a.sel[row] = make_uint4(0u, 0u, 0u, 0u);
+    return;
+  }
+
+  // ---- fast path --------------------------------------------------------------
+  __shared__ uint64_t cand[kCap];  // (key << 32) | index, sorted descending
+  __shared__ uint64_t csum[kCap];  // exclusive prefix sums of the exact masses
+  __shared__ uint32_t cnt_th[kNTheta];
+  __shared__ uint32_t ncand, nk_lo, nk_hi;
+  __shared__ int jsel[2];
+  __shared__ uint32_t n_eq;
+  __shared__ float red_l[kSelThreads / 64];
+  __shared__ uint64_t red_q[kSelThreads / 64];
+  __shared__ double red_d[kSelThreads / 64];
+  __shared__ int red_i[kSelThreads / 64];
+
+  if (tid < kNTheta) cnt_th[tid] = 0;
+  if (tid == 0) {
+    ncand = 0;
+    nk_lo = 0;
+    nk_hi = 0;
+    n_eq = 0;
+  }
+  __syncthreads();
+  // Counts of d = (xm - x) / T (fp32, equal to m - y when T == 1; close to
+  // it otherwise, the gather below checks the count) per bucket b: d <= theta_0 (b = 0),
+  // theta_(b-1) < d <= theta_b (b = 1..15), read off d's bits (exponent and
+  // first mantissa bit); a lane keeps them as 8-bit fields of two words (at
+  // most 16 * 8 entries between flushes).
+  {
+    uint32_t cth[kNTheta];
+#pragma unroll
+    for (int j = 0; j < kNTheta; ++j) cth[j] = 0;
+    uint64_t pk0 = 0, pk1 = 0;
+    int calls = 0;
+    float lsum = 0.f;  // top-p: sum of e^-d (fp32), for the choice of the head
+    uint32_t eq = 0;   // entries at the maximum (d == 0, mass 1 each)
+    auto flush = [&]() {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        cth[j] += (uint32_t)(pk0 >> (8 * j)) & 0xFFu;
+        cth[j + 8] += (uint32_t)(pk1 >> (8 * j)) & 0xFFu;
+      }
+      pk0 = 0;
+      pk1 = 0;
+    };
+    row_sweep<LT, kSelThreads, false>(x, 0, V, wp, [&](int64_t, const float(&y)[NV]) {
+#pragma unroll
+      for (int e = 0; e < NV; ++e) {
+        const float d = (xm - y[e]) * wp.rT;
+        const int b = min(max((((int)__float_as_uint(d) - 1) >> 22) - 249, 0), kNTheta);
+        const uint64_t inc = 1ull << (8 * (b & 7));
+        pk0 += b < 8 ? inc : 0ull;
+        pk1 += (b >= 8 && b < kNTheta) ? inc : 0ull;
+        if (use_p) {
+          lsum += __builtin_amdgcn_exp2f(d * -1.44269504088896341f);
+          eq += d == 0.f ? 1u : 0u;
+        }
+      }
+      if (++calls == 16) {
+        flush();
+        calls = 0;
+      }
+    });
+    flush();
+    // Cumulative: cth[j] = #{d <= theta_j}; then the block's sums.
+#pragma unroll
+    for (int j = 1; j < kNTheta; ++j) cth[j] += cth[j - 1];
+#pragma unroll
+    for (int j = 0; j < kNTheta; ++j) {
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) cth[j] += __shfl_xor(cth[j], o);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      lsum += __shfl_xor(lsum, o);
+      eq += __shfl_xor(eq, o);
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int j = 0; j < kNTheta; ++j) atomicAdd(&cnt_th[j], cth[j]);
+      atomicAdd(&n_eq, eq);
+      red_l[wv] = lsum;
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    // top-k alone: the narrowest head holding k.  top-p: first the narrowest
+    // head whose mass surely reaches top_p of the estimated total (entries at
+    // the maximum count 1, the others e^-theta of their bucket's bound), then
+    // the widest head that fits.
+    int j0 = -1, j1 = -1;
+    if (use_p) {
+      float L = 0.f;
+      for (int w = 0; w < kSelThreads / 64; ++w) L += red_l[w];
+      const float need = (float)a.top_p_q * 0x1p-32f * L * (1.f + 0x1p-8f);
+      float head = (float)n_eq + (float)(cnt_th[0] - n_eq) * __expf(-kTheta[0]);
+      for (int j = 0; j < kNTheta && cnt_th[j] <= (uint32_t)kCap; ++j) {
+        if (j > 0) head += (float)(cnt_th[j] - cnt_th[j - 1]) * __expf(-kTheta[j]);
+        if (j0 < 0 && head >= need) j0 = j;
+        j1 = j;
+      }
+      if (j0 < 0 || j0 == j1) {
+        j0 = j1;
+        j1 = -1;
+      }
+    } else {
+      for (int j = 0; j < kNTheta && j0 < 0; ++j)
+        if (cnt_th[j] >= (uint64_t)kk && cnt_th[j] <= (uint32_t)kCap) j0 = j;
+    }
+    jsel[0] = j0;
+    jsel[1] = j1;
+  }
+  __syncthreads();
+  for (int att = 0; att < 2 && jsel[att] >= 0; ++att) {
+    if (att > 0) {
+      if (tid == 0) {
+        ncand = 0;
+        nk_lo = 0;
+        nk_hi = 0;
+      }
+      __syncthreads();
+    }
+    const float ts = kTheta[jsel[att]];
+    // Gather the candidates; sum the fp32 masses of the others.
+    float tail = 0.f;
+    row_sweep<LT, kSelThreads>(x, 0, V, wp, [&](int64_t v0, const float(&y)[NV]) {
+      bool any = false;
+#pragma unroll
+      for (int e = 0; e < NV; ++e) {
+        const bool c = m - y[e] <= ts;  // a head of the order (monotone in y)
+        any |= c;
+        if (use_p && !c) tail += __builtin_amdgcn_exp2f((y[e] - m) * 1.44269504088896341f);
+      }
+      if (__ballot(any) == 0ull) return;
+#pragma unroll
+      for (int e = 0; e < NV; ++e) {
+        const bool c = m - y[e] <= ts;
+        const uint64_t bal = __ballot(c);
+        if (bal != 0ull) {
+          uint32_t base = 0;
+          if (lane == 0) base = atomicAdd(&ncand, (uint32_t)__popcll(bal));
+          base = __shfl(base, 0);
+          if (c) {
+            const uint32_t slot = base + (uint32_t)__popcll(bal & ((1ull << lane) - 1ull));
+            if (slot < (uint32_t)kCap) cand[slot] = ((uint64_t)ykey(y[e]) << 32) | (uint32_t)(v0 + e);
+          }
+        }
+      }
+    });
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) tail += __shfl_xor(tail, o);
+    if (lane == 0) red_f[wv] = tail;
+    __syncthreads();
+    const int n = min((int)ncand, kCap);
+    // The counts chose the threshold; these hold by construction.
+    const bool fits = (int)ncand <= kCap && (use_p || (int64_t)ncand >= kk);
+    float tail_all = 0.f;
+    for (int w = 0; w < kSelThreads / 64; ++w) tail_all += red_f[w];
+    // Bitonic sort, descending, padded with zero keys to a power of two.
+    int npad = 2;
+    while (npad < n) npad <<= 1;
+    for (int q = n + tid; q < npad; q += kSelThreads) cand[q] = 0ull;
+    __syncthreads();
+    for (int k2 = 2; k2 <= npad; k2 <<= 1)
+      for (int j2 = k2 >> 1; j2 > 0; j2 >>= 1) {
+        for (int q = tid; q < npad; q += kSelThreads) {
+          const int l = q ^ j2;
+          if (l > q) {
+            const uint64_t u = cand[q], w = cand[l];
+            if (((q & k2) == 0) ? (u < w) : (u > w)) {
+              cand[q] = w;
+              cand[l] = u;
+            }
+          }
+        }
+        __syncthreads();
+      }
+    // top-k: the k-th key when the candidates hold k (else every candidate
+    // passes top-k, and the cut comes from top-p inside the candidates).
+    const uint32_t tk = (kk > 0 && n >= kk) ? (uint32_t)(cand[kk - 1] >> 32) : 0u;
+    int nkeep = n;
+    bool ok = fits;
+    if (use_p && ok) {
+      // Exact masses along the order (thread tid holds entries EPT * tid ..
+      // + EPT - 1) and their exclusive prefix sums.
+      constexpr int EPT = kCap / kSelThreads;
+      uint64_t qv[EPT], tot = 0;
+#pragma unroll
+      for (int u = 0; u < EPT; ++u) {
+        const int e = EPT * tid + u;
+        qv[u] = e < n ? fixed_mass(key_to_y((uint32_t)(cand[e] >> 32)), m, S) : 0ull;
+        tot += qv[u];
+      }
+      uint64_t incl = tot;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint64_t y2 = __shfl_up(incl, o);
+        if (lane >= o) incl += y2;
+      }
+      if (lane == 63) red_q[wv] = incl;
+      __syncthreads();
+      uint64_t wbase = 0, H = 0;
+      for (int w = 0; w < kSelThreads / 64; ++w) {
+        if (w < wv) wbase += red_q[w];
+        H += red_q[w];
+      }
+      // L = H + (masses outside the candidates), bounded from the fp32 sum.
+      const double tr = (double)tail_all * __builtin_ldexp(1.0, S);
+      const double tlo = __builtin_fmax(0.0, tr * (1.0 - 0x1p-12) - (double)V);
+      const double thi = __builtin_fmin(tr * (1.0 + 0x1p-12) + (double)V + 1.0, 0x1p62);
+      const uint64_t tq_lo = tq_of(a.top_p_q, H + (uint64_t)__builtin_floor(tlo));
+      const uint64_t tq_hi = tq_of(a.top_p_q, H + (uint64_t)__builtin_ceil(thi));
+      uint32_t cl = 0, ch = 0;
+      uint64_t above = wbase + incl - tot;
+#pragma unroll
+      for (int u = 0; u < EPT; ++u) {
+        if (EPT * tid + u < n) {
+          cl += above < tq_lo;
+          ch += above < tq_hi;
+        }
+        above += qv[u];
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        cl += __shfl_xor(cl, o);
+        ch += __shfl_xor(ch, o);
+      }
+      if (lane == 0) {
+        atomicAdd(&nk_lo, cl);
+        atomicAdd(&nk_hi, ch);
+      }
+      __syncthreads();
+      // Decided: the first non-candidate (mass H above it) is dropped for
+      // every L in the bounds, and so is the same head of the candidates.
+      ok = H >= tq_hi && nk_lo == nk_hi;
+      nkeep = (int)nk_hi;
+    }
+    if (ok) {
+      double bz = -__builtin_huge_val();
+      int bi = -1;
+      for (int q = tid; q < n; q += kSelThreads) {
+        const uint64_t cv = cand[q];
+        const uint32_t key = (uint32_t)(cv >> 32);
+        const int v = (int)(uint32_t)cv;
+        if (q < nkeep && key >= tk) {
+          const double z = (double)key_to_y(key) + gumbel(draw_word(v, i, t, a.seed));
+          if (bi < 0 || z > bz || (z == bz && v < bi)) {
+            bz = z;
+            bi = v;
+          }
+        }
+      }
+      block_argmax(bz, bi, red_d, red_i, kSelThreads);
+      if (tid == 0) finish(bz, bi);
+      return;
+    }
+    __syncthreads();
+  }
+
+  // ---- radix selection over the whole row -------------------------------------
 
   // One radix pass: histogram of digit `shift` over the elements whose key
   // matches `prefix` above that digit (and, for the tie pass, key == tie_key
@@ -260,7 +751,7 @@ __global__ void __launch_bounds__(kSelThreads) sample_select_kernel(const Accept
     __syncthreads();
     const uint32_t hi_mask = shift >= 24 ? 0u : ~((1u << (shift + 8)) - 1u);
     for (int v = tid; v < V; v += kSelThreads) {
-      const float y = warp_y<LT>(x[v], a.temperature);
+      const float y = warp_y<LT>(x[v], wp);
       const uint32_t k = ykey(y);
       uint32_t src = k;
       if (by_index) {
@@ -407,51 +898,69 @@ __global__ void __launch_bounds__(kSweepThreads) sample_sweep_kernel(const Accep
   const int t = (int)(row / a.M), i = (int)(row % a.M);
   const LT* x = reinterpret_cast<const LT*>(a.logits) + (int64_t)t * a.l_st + (int64_t)i * a.l_sm;
   const int64_t lo = (int64_t)c * a.chunk, hi = min(lo + a.chunk, a.V);
+  const Warp wp = make_warp(a.temperature);
   uint32_t tk = 0, ystar = 0, istar = 0;
   if (a.sel != nullptr) {
     const uint4 s = a.sel[row];
+    if (s.w != 0) return;  // drawn by the select kernel
     tk = s.x;
     ystar = s.y;
     istar = s.z;
   }
+  const uint32_t k0 = (uint32_t)a.seed, k1 = (uint32_t)(a.seed >> 32);
   double best = -__builtin_huge_val();
   int bi = -1;
-  for (int64_t v = lo + threadIdx.x; v < hi; v += kSweepThreads) {
-    const float y = warp_y<LT>(x[v], a.temperature);
-    if (!(y > kNegInfF)) continue;
-    const uint32_t k = ykey(y);
-    if (k < tk || k < ystar || (k == ystar && (uint32_t)v < istar)) continue;
-    const double g = gumbel(philox_word0((uint64_t)v, (uint64_t)i, (uint64_t)t, 0ull, a.seed, 0ull));
-    const double z = (double)y + g;
-    if (bi < 0 || z > best) {
-      best = z;
-      bi = (int)v;
-    }
-  }
-  // Reduction: larger z, then lower index; -1 = nothing kept.
+  float lb = kNegInfF;   // wave-uniform lower bound of the range's maximum z
+  float lbl = kNegInfF;  // this lane's share of it
+  // Every lane of a wave runs the same iterations (the bound is shared by
+  // shuffles); a vector of NV entries is NV / 4 generator groups.
+  constexpr int NV = 16 / sizeof(LT);
+  row_sweep<LT, kSweepThreads>(x, lo, hi, wp, [&](int64_t v0, const float(&yv)[NV]) {
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const double ob = __shfl_xor(best, o);
-    const int oi = __shfl_xor(bi, o);
-    if (oi >= 0 && (bi < 0 || ob > best || (ob == best && oi < bi))) {
-      best = ob;
-      bi = oi;
+    for (int gq = 0; gq < NV / 4; ++gq) {
+      const int64_t g = v0 + 4 * gq;
+      bool kp[4];
+      float ym = kNegInfF;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float yy = yv[4 * gq + e];
+        const uint32_t k = ykey(yy);
+        kp[e] = yy > kNegInfF && k >= tk && (k > ystar || (k == ystar && (uint32_t)(g + e) >= istar));
+        if (kp[e]) ym = fmaxf(ym, yy);
+      }
+      // G < kGumbelMax: a group whose largest kept y cannot reach the bound
+      // holds no winner and needs no generator call.
+      if (ym > kNegInfF && ym + kGumbelMax + kZMargin + (fabsf(ym) + kGumbelMax) * kZMarginRel >= lb) {
+        const uint4 w4 = philox4x32((uint32_t)(g >> 2), (uint32_t)i, (uint32_t)t, 0u, k0, k1);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (!kp[e]) continue;
+          const float yy = yv[4 * gq + e];
+          const uint32_t w = word_of(w4, e);
+          const float zf = yy + gumbel_est(w);
+          const float mg = kZMargin + fabsf(zf) * kZMarginRel;
+          lbl = fmaxf(lbl, zf - mg);
+          if (zf + mg >= lb) {
+            // Within the margin of the bound: the exact draw (entries of a
+            // lane come in increasing index, so a tie keeps the first).
+            const double z = (double)yy + gumbel(w);
+            if (bi < 0 || z > best) {
+              best = z;
+              bi = (int)(g + e);
+            }
+          }
+        }
+      }
     }
-  }
+    float wl = lbl;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) wl = fmaxf(wl, __shfl_xor(wl, o));
+    lb = wl;
+  });
   __shared__ double sb[kSweepThreads / 64];
   __shared__ int si[kSweepThreads / 64];
-  const int w = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) {
-    sb[w] = best;
-    si[w] = bi;
-  }
-  __syncthreads();
+  block_argmax(best, bi, sb, si, kSweepThreads);
   if (threadIdx.x == 0) {
-    for (int k = 1; k < kSweepThreads / 64; ++k)
-      if (si[k] >= 0 && (bi < 0 || sb[k] > best || (sb[k] == best && si[k] < bi))) {
-        best = sb[k];
-        bi = si[k];
-      }
     const uint64_t zb = __builtin_bit_cast(uint64_t, best);
     a.rstat[row * a.nchunk + c] =
         make_float4(__uint_as_float((uint32_t)zb), __uint_as_float((uint32_t)(zb >> 32)), __int_as_float(bi), 0.f);

@@ -52,6 +52,20 @@ def test_sample_full_vocab_64_nodes(gpu):
     run_and_compare(a.logits, a.draft, a.parent_ref, a.pos, 8, 1.0, 1.0, 0, seed=7)
 
 
+@pytest.mark.parametrize("sigma,top_p,top_k", [(0.3, 0.9, 0), (0.3, 1.0, 3000), (3.0, 1.0, 2000), (3.0, 0.999, 0),
+                                             (3.0, 0.5, 7)])
+def test_sample_full_vocab_flat_and_peaked_rows(gpu, sigma, top_p, top_k):
+    """bf16 [1, 16, 128256] N(0, sigma) logits: flat rows whose top-p set or
+    top-k is too large for the select kernel's candidate list (the radix
+    selection and the sweep draw them), and peaked rows drawn from the
+    candidates."""
+    print(f"[sample] full vocab sigma={sigma} top_p={top_p} top_k={top_k}", flush=True)
+    a = wl.make_accept_inputs(T=1, M=16, V=128256, device=str(gpu), seed=31)
+    g = torch.Generator().manual_seed(31)
+    lg = (torch.randn((1, 16, 128256), generator=g) * sigma).to(torch.bfloat16).to(gpu)  # no planted token
+    run_and_compare(lg, a.draft, a.parent_ref, a.pos, 8, 1.0, top_p, top_k, seed=77)
+
+
 def test_sample_ties_at_the_top_p_cut(gpu):
     """bf16 rows of a few repeated values, so the top-p cut falls inside a tie
     group (kept: its highest indices) and top-k ties are all kept."""

@@ -1,6 +1,6 @@
 """The sampling oracle (oracle/sampling.py) pinned without the GPU.
 
-  * its counter RNG against numpy.random.Philox (Philox4x64-10), word for word;
+  * its counter RNG against the Random123 known-answer vectors of Philox4x32-10;
   * its deterministic ln / 2^x against numpy's log / exp2 (a few ulp);
   * its warpers against transformers' own TemperatureLogitsWarper /
     TopPLogitsWarper / TopKLogitsWarper on the committed fixture rows
@@ -24,19 +24,30 @@ from oracle import sampling as sp
 GOLDEN = Path(__file__).resolve().parent / "golden" / "sampling_warpers.json"
 
 
-@pytest.mark.parametrize("key", [(0, 0), (0x0123456789ABCDEF, 0), (2 ** 64 - 1, 2 ** 64 - 1), (7, 3)])
-def test_philox_matches_numpy_bit_generator(key):
-    # numpy's Philox bumps the counter before each block: block j uses counter j + 1.
-    bg = np.random.Philox(key=np.array(key, dtype=np.uint64))
-    raw = bg.random_raw(4 * 6).reshape(6, 4)
-    got = sp.philox4x64_10(np.arange(1, 7, dtype=np.uint64), 0, 0, 0, key[0], key[1])
-    for w in range(4):
-        assert np.array_equal(got[w], raw[:, w])
-    # higher counter words too
-    bg = np.random.Philox(key=np.array(key, dtype=np.uint64), counter=np.array([2 ** 64 - 1, 5, 9, 0], dtype=np.uint64))
-    raw = bg.random_raw(4)
-    got = sp.philox4x64_10(np.array([0], dtype=np.uint64), 6, 9, 0, key[0], key[1])
-    assert [int(g[0]) for g in got] == [int(r) for r in raw]
+# Known-answer vectors of philox4x32_10 published with the Random123 library
+# (Salmon et al. 2011): (counter, key) -> output block.
+PHILOX4X32_KAT = [
+    ((0x00000000, 0x00000000, 0x00000000, 0x00000000), (0x00000000, 0x00000000),
+     (0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8)),
+    ((0xFFFFFFFF, 0xFFFFFFFF, 0xFFFFFFFF, 0xFFFFFFFF), (0xFFFFFFFF, 0xFFFFFFFF),
+     (0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD)),
+    ((0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344), (0xA4093822, 0x299F31D0),
+     (0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1)),
+]
+
+
+@pytest.mark.parametrize("ctr,key,want", PHILOX4X32_KAT)
+def test_philox_known_answer_vectors(ctr, key, want):
+    got = sp.philox4x32_10(*[np.array([c], dtype=np.uint64) for c in ctr], *key)
+    assert [int(g[0]) for g in got] == list(want)
+
+
+def test_uniforms_use_one_word_per_element_of_a_four_element_group():
+    seed, tree, node = 0x0123456789ABCDEF, 3, 7
+    u = sp.uniforms(seed, tree, node, 10)
+    for v in range(10):
+        w = sp.philox4x32_10(np.array([v >> 2], dtype=np.uint64), node, tree, 0, seed & 0xFFFFFFFF, seed >> 32)
+        assert u[v] == (float(w[v & 3][0]) + 0.5) * 2.0 ** -32
 
 
 def test_uniforms_are_open_unit_interval_and_uniform():
