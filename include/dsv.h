@@ -282,8 +282,9 @@ int dsv_tree_accept(int mode, const dsv_tensor* logits, const dsv_tensor* draft,
  * descending index" whose probability mass reaches top_p, the masses taken
  * as exact 64-bit fixed-point integers; top-k (applied when > 0) keeps
  * y >= the k-th largest y.  The draw per node is a counter-based Gumbel-max
- * over the kept tokens: argmax of y + G, G = -ln(-ln U), U from
- * Philox4x64-10 with key (seed, 0) and counter (token, node, tree, 0), the
+ * over the kept tokens: argmax of y + G, G = -ln(-ln U), U = (w + 0.5) 2^-32
+ * with w the output word token & 3 of Philox4x32-10 at key (seed mod 2^32,
+ * seed >> 32) and counter (token >> 2, node, tree, 0), the
  * logarithms evaluated with a fixed sequence of correctly rounded double
  * operations, so the draws are reproducible bit for bit; they are samples of
  * softmax(y) over the kept set.  A row without a finite logit draws token 0.

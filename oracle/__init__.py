@@ -26,7 +26,8 @@ Pinning (what each function is checked against, besides the GPU):
                         full accept, root only) — tests/test_oracle_accept.py
   bundles.packing_order the reference's scheduler vectors, hand-worked orders,
                         invariants on generated trees — tests/test_oracle_bundles.py
-  sampling              numpy.random.Philox (the counter RNG), numpy's log/exp2
+  sampling              Random123's known-answer vectors of Philox4x32-10 (the
+                        counter RNG), numpy's log/exp2
                         (the deterministic ln / 2^x), transformers' own warpers on
                         committed fixture rows (tests/golden/sampling_warpers.json),
                         an independent float nucleus, chi-square of the draws
