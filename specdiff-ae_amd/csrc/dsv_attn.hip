@@ -665,12 +665,17 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
   }
 
   // ---- epilogue: normalised bf16 partial + (max, sum) per row ----------------
+  // After this barrier no wave reads the ring any more.  Each wave stages its
+  // 32 partial rows there (16-byte chunks XOR-swizzled by row, against bank
+  // conflicts) and writes its contiguous block of rows with whole 16-byte
+  // lanes: one KiB of consecutive bytes per store instruction.
+  __syncthreads();
   if (!wave_active) return;
   const float ltot = xor32_sum(lsum);
-  if (!rvalid) return;
-  const int64_t prow = (((int64_t)split * a.B + b) * a.Hk + kvh) * a.R + r_me;
   const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
-  uint16_t* op = a.opart + prow * D;
+  constexpr int CHR = D / 8;  // 16-byte chunks per row
+  static_assert(NW * 32 * D * 2 <= G::RING, "the partial rows of all waves fit the ring");
+  uint8_t* stage = smem + wid * (32 * D * 2);
   // Accumulator value v of d tile dt holds d = 32*dt + 8*(v/4) + 4*lg + v%4.
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) {
@@ -679,10 +684,20 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
       const f32x16 x = acc[dt];
       const u32x2 val = {pack2<BF16>(x[4 * q4] * inv, x[4 * q4 + 1] * inv),
                          pack2<BF16>(x[4 * q4 + 2] * inv, x[4 * q4 + 3] * inv)};
-      *reinterpret_cast<u32x2*>(op + dt * 32 + 8 * q4 + 4 * lg) = val;
+      const int c = 4 * dt + q4;
+      *reinterpret_cast<u32x2*>(stage + lj * (2 * D) + ((c ^ (lj % CHR)) * 16) + 8 * lg) = val;
     }
   }
-  if (lg == 0) a.ml[prow] = make_float2(mx, ltot);
+  const int64_t pbase = (((int64_t)split * a.B + b) * a.Hk + kvh) * a.R + row0;
+  uint16_t* op = a.opart + pbase * D;
+#pragma unroll
+  for (int k = 0; k < CHR / 2; ++k) {
+    const int f = k * 64 + lane, r = f / CHR, i = f % CHR;
+    if (row0 + r < a.R)
+      *reinterpret_cast<u32x4*>(op + (int64_t)r * D + i * 8) =
+          *reinterpret_cast<const u32x4*>(stage + r * (2 * D) + ((i ^ (r % CHR)) * 16));
+  }
+  if (rvalid && lg == 0) a.ml[pbase + lj] = make_float2(mx, ltot);
 }
 
 // A launch with timing events records them from the kernel's own dispatch
