@@ -487,7 +487,6 @@ __global__ void __launch_bounds__(kSelThreads) sample_select_kernel(const Accept
 
   // ---- fast path --------------------------------------------------------------
   __shared__ uint64_t cand[kCap];  // (key << 32) | index, sorted descending
-  __shared__ uint64_t csum[kCap];  // exclusive prefix sums of the exact masses
   __shared__ uint32_t cnt_th[kNTheta];
   __shared__ uint32_t ncand, nk_lo, nk_hi;
   __shared__ int jsel[2];
@@ -636,7 +635,8 @@ __global__ void __launch_bounds__(kSelThreads) sample_select_kernel(const Accept
     if (lane == 0) red_f[wv] = tail;
     __syncthreads();
     const int n = min((int)ncand, kCap);
-    // The counts chose the threshold; these hold by construction.
+    // The counts (of the unwarped logits when T != 1) chose the threshold;
+    // the gathered count decides whether the head fits and holds k entries.
     const bool fits = (int)ncand <= kCap && (use_p || (int64_t)ncand >= kk);
     float tail_all = 0.f;
     for (int w = 0; w < kSelThreads / 64; ++w) tail_all += red_f[w];
