@@ -79,12 +79,18 @@ def test_tree_verify_graph_replays(gpu):
                                                      page_table=other.page_table))
 
 
-@pytest.mark.parametrize("mode", ["greedy", "typical"])
-def test_tree_accept_graph_replays(gpu, mode):
-    print(f"[graph] tree_accept {mode}", flush=True)
+_ACCEPT_KW = {"greedy": ("greedy", {}),
+              "typical": ("typical", dict(temperature=1.0, posterior_threshold=0.09, posterior_alpha=0.3)),
+              "sample_top_p_top_k": ("sample", dict(temperature=0.7, top_p=0.9, top_k=50, seed=11)),
+              "sample_temperature": ("sample", dict(temperature=1.3, seed=12))}
+
+
+@pytest.mark.parametrize("case", list(_ACCEPT_KW))
+def test_tree_accept_graph_replays(gpu, case):
+    print(f"[graph] tree_accept {case}", flush=True)
     a = wl.make_accept_inputs(T=4, M=32, V=5000, device=str(gpu), seed=3)
     b = wl.make_accept_inputs(T=2, M=16, V=3000, device=str(gpu), seed=4)
-    kw = dict(temperature=1.0, posterior_threshold=0.09, posterior_alpha=0.3) if mode == "typical" else {}
+    mode, kw = _ACCEPT_KW[case]
 
     def fn():
         return tree_accept(a.logits, a.draft, a.parent_ref, a.pos, 10, mode=mode, return_next=True, **kw)
