@@ -750,19 +750,17 @@ __global__ void __launch_bounds__(kSelThreads) sample_select_kernel(const Accept
     if (tid < 256) hist[tid] = 0;
     __syncthreads();
     const uint32_t hi_mask = shift >= 24 ? 0u : ~((1u << (shift + 8)) - 1u);
-    for (int v = tid; v < V; v += kSelThreads) {
-      const float y = warp_y<LT>(x[v], wp);
-      const uint32_t k = ykey(y);
-      uint32_t src = k;
-      if (by_index) {
-        if (k != tie_key) continue;
-        src = (uint32_t)v;
+    row_sweep<LT, kSelThreads>(x, 0, V, wp, [&](int64_t v0, const float(&y)[NV]) {
+#pragma unroll
+      for (int e = 0; e < NV; ++e) {
+        const uint32_t k = ykey(y[e]);
+        const uint32_t src = by_index ? (uint32_t)(v0 + e) : k;
+        const bool valid = v0 + e < V && (!by_index || k == tie_key) && (src & hi_mask) == (prefix & hi_mask);
+        if (valid)
+          atomicAdd(reinterpret_cast<unsigned long long*>(&hist[(src >> shift) & 255u]),
+                    (unsigned long long)(mass ? fixed_mass(y[e], m, S) : 1ull));
       }
-      if ((src & hi_mask) != (prefix & hi_mask)) continue;
-      const int bin = (int)((src >> shift) & 255u);
-      atomicAdd(reinterpret_cast<unsigned long long*>(&hist[bin]),
-                (unsigned long long)(mass ? fixed_mass(y, m, S) : 1ull));
-    }
+    });
     __syncthreads();
   };
 
@@ -797,7 +795,16 @@ __global__ void __launch_bounds__(kSelThreads) sample_select_kernel(const Accept
     uint64_t above = 0, Tq = 0, group = 0;
     for (int d = 0; d < ND; ++d) {
       const int shift = 24 - 8 * d;
-      pass(shift, prefix, true, false, 0);
+      if (d > 0 && d == ND - 1) {
+        // The last digit completes the key: every bin holds one value of y,
+        // so its mass is its count times that value's mass.
+        pass(shift, prefix, false, false, 0);
+        if (tid < 256 && hist[tid] != 0ull)
+          hist[tid] *= fixed_mass(key_to_y(fill_low(prefix | ((uint32_t)tid << shift), ND)), m, S);
+        __syncthreads();
+      } else {
+        pass(shift, prefix, true, false, 0);
+      }
       if (d == 0 && tid < 64) {
         // Total mass L and the threshold Tq = ceil(P * L / 2^32).
         uint64_t s = hist[4 * tid] + hist[4 * tid + 1] + hist[4 * tid + 2] + hist[4 * tid + 3];
