@@ -138,6 +138,36 @@ def test_accept_validation(dsv_lib):
     assert rc == -1 and "tree count" in _ext.last_error()
 
 
+def test_accept_sample_validation(dsv_lib):
+    """The sampling entry point checks its warper arguments and workspace
+    before any launch (the fake tensors are never dereferenced)."""
+    logits = _t((2, 8, 100), _ext.DSV_BF16)
+    draft = _t((2, 8), _ext.DSV_I64)
+    parent = _t((2, 7), _ext.DSV_I64)
+    pos = _t((8,), _ext.DSV_I64)
+    o = _t((2, 8), _ext.DSV_I64)
+    info = _t((2, 4), _ext.DSV_I64)
+    none = _ext.DsvTensor()
+
+    def call(temperature=1.0, top_p=1.0, top_k=0, ws=None, nbytes=0, lg=logits):
+        return dsv_lib.dsv_tree_accept_sample(ctypes.byref(lg), ctypes.byref(draft), ctypes.byref(parent),
+                                              ctypes.byref(pos), 10, temperature, top_p, top_k, 5, ctypes.byref(o),
+                                              ctypes.byref(o), ctypes.byref(info), ctypes.byref(none), ws, nbytes,
+                                              None)
+
+    assert call(temperature=0.0) == -1 and "temperature" in _ext.last_error()
+    assert call(temperature=float("nan")) == -1 and "temperature" in _ext.last_error()
+    assert call(top_p=1.5) == -1 and "top_p" in _ext.last_error()
+    assert call(top_p=-0.1) == -1 and "top_p" in _ext.last_error()
+    assert call(top_k=-1) == -1 and "top_k" in _ext.last_error()
+    assert call(lg=_t((2, 8, 100), _ext.DSV_I32)) == -1 and "logits" in _ext.last_error()
+    rc = call(ws=0x1000, nbytes=16)
+    assert rc == -3 and "workspace" in _ext.last_error()  # DSV_ERR_WORKSPACE
+    need = dsv_lib.dsv_accept_workspace_bytes(2, 8, 100)
+    rc = call(ws=0x1000 + 16, nbytes=need)
+    assert rc == -3 and "aligned" in _ext.last_error()
+
+
 def test_kv_commit_validation(dsv_lib):
     path = _t((1, 8), _ext.DSV_I64)
     info = _t((1, 4), _ext.DSV_I64)
