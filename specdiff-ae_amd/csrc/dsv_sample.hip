@@ -22,20 +22,23 @@
 //
 // Kernels:
 //   sample_select_kernel  one workgroup per row, only with top-p or top-k.
-//       Fast path: the row maximum m, then counts of y >= m - theta_j for a
-//       ladder of thetas (wave ballots), then the candidates y >= m - theta*
-//       (at most kCap, a head of the order) are gathered into LDS and sorted.
-//       top-k is the candidates' k-th key; top-p takes the exact masses of
-//       the candidates and bounds the rest of L by an fp32 sum (relative
-//       error far below the 2^-12 allowed): the cut is exact whenever it lies
-//       inside the candidates for every L in those bounds.  The draw is then
-//       taken over the kept candidates and written as the row's result.
-//       Otherwise (a flat row, a large k, an undecided cut): 8-bit radix
+//       The row maximum m; counts of d = m - y in a ladder of buckets (read
+//       off d's bits); the narrowest head {d <= theta} (at most kCap
+//       entries) that surely carries the top-p mass, or holds k entries, is
+//       gathered into LDS and sorted.  top-k is the head's k-th key; top-p
+//       takes the head's exact masses and bounds the rest of L by an fp32
+//       sum: the cut is exact when it lands on the same entry for every L in
+//       those bounds, inside the head.  The draw over the kept head entries is
+//       the row's result.  Other rows (flat rows, a large k, an undecided
+//       cut) are left to the radix kernel (status 2, with m).
+//   sample_radix_kernel   one workgroup per row left open: 8-bit radix
 //       selection over the order keys of y (count-weighted for top-k,
-//       mass-weighted for top-p), then over the indices of the tie group at
-//       the top-p cut; the kept-set bounds go to the sweep.
+//       mass-weighted for top-p); the kept set (keys at or above both bounds)
+//       is gathered into LDS, where the index bound in the cut's tie group and
+//       the draw are taken when it fits; otherwise the bound comes from index
+//       passes over the row and the sweep draws.
 //   sample_sweep_kernel   one workgroup per (row, vocabulary range) of the
-//       rows the select kernel left open (all rows without top-p / top-k):
+//       rows still open (all rows without top-p / top-k):
 //       the Gumbel-max draw over the range's kept entries.  An fp32 estimate
 //       of each z (within 2^-14 of it) against a wave-shared lower bound of
 //       the range's maximum z leaves the exact double evaluation to the few
@@ -434,10 +437,7 @@ __global__ void __launch_bounds__(kSelThreads) sample_select_kernel(const Accept
   constexpr int ND = key_digits<LT>();
   const Warp wp = make_warp(a.temperature);
 
-  __shared__ uint64_t hist[256];
   __shared__ float red_f[kSelThreads / 64];
-  __shared__ uint32_t res_u[4];
-  __shared__ uint64_t res_q[4];
 
   // Row maximum of y: the warper is monotone, so it is the warped maximum
   // logit (xm).
@@ -741,6 +741,50 @@ __global__ void __launch_bounds__(kSelThreads) sample_select_kernel(const Accept
     __syncthreads();
   }
 
+  // ---- not decided here: the radix kernel takes the row (status 2, with m) --
+  if (tid == 0) a.sel[row] = make_uint4(__float_as_uint(m), 0u, 0u, 2u);
+}
+
+// Radix selection for the rows the select kernel left open (status 2): the
+// top-k key, the top-p cut key and, in the cut's tie group, the index bound;
+// the kept set is then gathered and drawn here when it fits in LDS, else the
+// bounds go to the sweep kernel.
+template <typename LT>
+__global__ void __launch_bounds__(kSelThreads) sample_radix_kernel(const AcceptArgs a) {
+  const int64_t row = blockIdx.x;
+  const uint4 st = a.sel[row];
+  if (st.w != 2u) return;
+  const int t = (int)(row / a.M), i = (int)(row % a.M);
+  const LT* x = reinterpret_cast<const LT*>(a.logits) + (int64_t)t * a.l_st + (int64_t)i * a.l_sm;
+  const int V = (int)a.V;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  constexpr int ND = key_digits<LT>();
+  constexpr int NV = 16 / sizeof(LT);
+  const Warp wp = make_warp(a.temperature);
+  const float m = __uint_as_float(st.x);  // the row maximum of y, from the select kernel
+  int S = 63;
+  for (int vv = V; vv > 0; vv >>= 1) --S;  // 63 - bitlen(V)
+  const int64_t kk = (a.top_k > 0 && a.top_k < V) ? a.top_k : 0;
+  const bool use_p = a.top_p_q != 0;
+  (void)kk;
+
+  __shared__ uint64_t hist[256];
+  __shared__ uint32_t res_u[4];
+  __shared__ uint64_t res_q[4];
+  __shared__ uint64_t cand[kCap];
+  __shared__ uint32_t ncand, nk_lo;
+  __shared__ double red_d[kSelThreads / 64];
+  __shared__ int red_i[kSelThreads / 64];
+  auto finish = [&](double z, int idx) {
+    const uint64_t zb = __builtin_bit_cast(uint64_t, z);
+    for (int c = 0; c < a.nchunk; ++c)
+      a.rstat[row * a.nchunk + c] =
+          c == 0 ? make_float4(__uint_as_float((uint32_t)zb), __uint_as_float((uint32_t)(zb >> 32)), __int_as_float(idx), 0.f)
+                 : make_float4(0.f, 0.f, __int_as_float(-1), 0.f);
+    a.sel[row] = make_uint4(0u, 0u, 0u, 1u);
+  };
+
   // ---- radix selection over the whole row -------------------------------------
 
   // One radix pass: histogram of digit `shift` over the elements whose key
@@ -788,11 +832,12 @@ __global__ void __launch_bounds__(kSelThreads) sample_select_kernel(const Accept
     tk = fill_low(prefix, ND);
   }
 
-  // top-p: the key of the last kept element, then the index bound in its tie group.
+  // top-p: the key of the last kept element (ystar), then the index bound in
+  // its tie group (istar).
   uint32_t ystar = 0, istar = 0;
-  if (a.top_p_q != 0) {
+  uint64_t above = 0, Tq = 0;
+  if (use_p) {
     uint32_t prefix = 0;
-    uint64_t above = 0, Tq = 0, group = 0;
     for (int d = 0; d < ND; ++d) {
       const int shift = 24 - 8 * d;
       if (d > 0 && d == ND - 1) {
@@ -810,13 +855,7 @@ __global__ void __launch_bounds__(kSelThreads) sample_select_kernel(const Accept
         uint64_t s = hist[4 * tid] + hist[4 * tid + 1] + hist[4 * tid + 2] + hist[4 * tid + 3];
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
-        if (tid == 0) {
-          const uint64_t P = a.top_p_q;
-          const uint64_t lo = P * s, hi = __umul64hi(P, s);
-          const uint64_t lo2 = lo + 0xFFFFFFFFull;
-          const uint64_t hi2 = hi + (lo2 < lo ? 1ull : 0ull);
-          res_q[1] = (lo2 >> 32) | (hi2 << 32);
-        }
+        if (tid == 0) res_q[1] = tq_of(a.top_p_q, s);
       }
       __syncthreads();
       Tq = res_q[1];
@@ -828,7 +867,6 @@ __global__ void __launch_bounds__(kSelThreads) sample_select_kernel(const Accept
           res_u[0] = (uint32_t)(b < 0 ? 255 : b);
           res_u[1] = b < 0 ? 1u : 0u;
           res_q[0] = before;
-          res_q[2] = b < 0 ? 0 : hist[b];  // mass of the chosen bin
         }
       }
       __syncthreads();
@@ -842,57 +880,139 @@ __global__ void __launch_bounds__(kSelThreads) sample_select_kernel(const Accept
       }
     }
     ystar = prefix == 0xFFFFFFFFu ? prefix : fill_low(prefix, ND);
-    if (ystar != 0xFFFFFFFFu) {
-      // Tie group of the cut key: its size c and per-element mass q*.
-      float ys;
-      {
-        const uint32_t b = ystar ^ ((ystar >> 31) ? 0x80000000u : 0xFFFFFFFFu);
-        ys = __uint_as_float(b);
-      }
-      const uint64_t qs = fixed_mass(ys, m, S);
-      // Group size: count pass on the exact key (every index in bin 0).
-      pass(24, 0, false, true, ystar);
+  }
+  if (ystar == 0xFFFFFFFFu) {  // nothing is kept
+    if (tid == 0) a.sel[row] = make_uint4(tk, ystar, 0u, 0u);
+    return;
+  }
+  // Mass q* of one member of the cut's tie group, and how many of the group
+  // (its highest indices) the cut keeps: n_keep = #{j : above + j q* < Tq}.
+  const uint64_t qs = use_p ? fixed_mass(key_to_y(ystar), m, S) : 0ull;
+  auto keep_of = [&](uint64_t group) -> uint64_t {
+    if (!use_p || qs == 0) return group;
+    const uint64_t need = (Tq - above + qs - 1) / qs;
+    return need < group ? need : group;
+  };
+  // The index bound among the tie members: the rank-th largest index, digit
+  // by digit (8-bit digits over bitlen(V - 1) bits); count(shift, prefix)
+  // fills hist with the digit counts of the members that match prefix above.
+  auto index_bound = [&](uint64_t rank, auto&& count) -> uint32_t {
+    int ib = 0;
+    for (int vv = V - 1; vv > 0; vv >>= 1) ++ib;
+    uint32_t ipre = 0;
+    for (int d = (ib + 7) / 8 - 1; d >= 0; --d) {
+      const int shift = 8 * d;
+      count(shift, ipre);
       if (tid < 64) {
-        uint64_t c = hist[4 * tid] + hist[4 * tid + 1] + hist[4 * tid + 2] + hist[4 * tid + 3];
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o);
-        if (tid == 0) res_q[3] = c;
-      }
-      __syncthreads();
-      group = res_q[3];
-      __syncthreads();
-      // Index-bit passes cover bitlen(V - 1) bits: the kept members are the
-      // n_keep highest indices, n_keep = #{j < c : above + j q* < Tq}.
-      uint64_t n_keep = group;
-      if (qs > 0) {
-        const uint64_t need = (Tq - above + qs - 1) / qs;
-        n_keep = need < group ? need : group;
-      }
-      if (n_keep < group) {
-        int ib = 0;
-        for (int vv = V - 1; vv > 0; vv >>= 1) ++ib;
-        const int nd_i = (ib + 7) / 8;
-        uint32_t ipre = 0;
-        uint64_t rank = n_keep;
-        for (int d = nd_i - 1; d >= 0; --d) {
-          const int shift = 8 * d;
-          pass(shift, ipre, false, true, ystar);
-          if (tid < 64) {
-            uint64_t before = 0;
-            const int b = scan_desc(hist, rank, before);
-            if (tid == 0) {
-              res_u[0] = (uint32_t)max(b, 0);
-              res_q[0] = before;
-            }
-          }
-          __syncthreads();
-          ipre |= res_u[0] << shift;
-          rank -= res_q[0];
-          __syncthreads();
+        uint64_t before = 0;
+        const int b = scan_desc(hist, rank, before);
+        if (tid == 0) {
+          res_u[0] = (uint32_t)max(b, 0);
+          res_q[0] = before;
         }
-        istar = ipre;
       }
+      __syncthreads();
+      ipre |= res_u[0] << shift;
+      rank -= res_q[0];
+      __syncthreads();
     }
+    return ipre;
+  };
+
+  // ---- the kept set in LDS: every entry with key >= max(tk, ystar) ----------
+  // When it fits, the tie bound and the draw are taken here; otherwise the
+  // bounds go to the sweep kernel.
+  {
+    const uint32_t lower = max(tk, ystar);
+    uint32_t* list = reinterpret_cast<uint32_t*>(cand);  // kList indices
+    constexpr int kList = 2 * kCap;
+    if (tid == 0) ncand = 0;
+    __syncthreads();
+    row_sweep<LT, kSelThreads>(x, 0, V, wp, [&](int64_t v0, const float(&y)[NV]) {
+      bool any = false;
+#pragma unroll
+      for (int e = 0; e < NV; ++e) any |= v0 + e < V && ykey(y[e]) >= lower;
+      if (__ballot(any) == 0ull) return;
+#pragma unroll
+      for (int e = 0; e < NV; ++e) {
+        const bool c = v0 + e < V && ykey(y[e]) >= lower;
+        const uint64_t bal = __ballot(c);
+        if (bal != 0ull) {
+          uint32_t base = 0;
+          if (lane == 0) base = atomicAdd(&ncand, (uint32_t)__popcll(bal));
+          base = __shfl(base, 0);
+          if (c) {
+            const uint32_t slot = base + (uint32_t)__popcll(bal & ((1ull << lane) - 1ull));
+            if (slot < (uint32_t)kList) list[slot] = (uint32_t)(v0 + e);
+          }
+        }
+      }
+    });
+    __syncthreads();
+    const int nl = (int)ncand;
+    if (nl <= kList) {
+      auto key_at = [&](int q) { return ykey(warp_y<LT>(x[list[q]], wp)); };
+      if (use_p && ystar >= tk) {
+        uint32_t g = 0;
+        for (int q = tid; q < nl; q += kSelThreads) g += key_at(q) == ystar ? 1u : 0u;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) g += __shfl_xor(g, o);
+        if (tid == 0) nk_lo = 0;
+        __syncthreads();
+        if (lane == 0) atomicAdd(&nk_lo, g);
+        __syncthreads();
+        const uint64_t group = nk_lo;
+        const uint64_t n_keep = keep_of(group);
+        if (n_keep < group)
+          istar = index_bound(n_keep, [&](int shift, uint32_t ipre) {
+            if (tid < 256) hist[tid] = 0;
+            __syncthreads();
+            const uint32_t hi_mask = shift >= 24 ? 0u : ~((1u << (shift + 8)) - 1u);
+            for (int q = tid; q < nl; q += kSelThreads) {
+              const uint32_t v = list[q];
+              if (key_at(q) == ystar && (v & hi_mask) == (ipre & hi_mask))
+                atomicAdd(reinterpret_cast<unsigned long long*>(&hist[(v >> shift) & 255u]), 1ull);
+            }
+            __syncthreads();
+          });
+      }
+      double bz = -__builtin_huge_val();
+      int bi = -1;
+      for (int q = tid; q < nl; q += kSelThreads) {
+        const int v = (int)list[q];
+        const float y = warp_y<LT>(x[v], wp);
+        const uint32_t k = ykey(y);
+        if (k >= tk && (k > ystar || (k == ystar && (uint32_t)v >= istar))) {
+          const double z = (double)y + gumbel(draw_word(v, i, t, a.seed));
+          if (bi < 0 || z > bz || (z == bz && v < bi)) {
+            bz = z;
+            bi = v;
+          }
+        }
+      }
+      block_argmax(bz, bi, red_d, red_i, kSelThreads);
+      if (tid == 0) finish(bz, bi);
+      return;
+    }
+  }
+
+  // ---- the kept set is too large: tie bound by passes over the row, then the
+  // sweep draws with the bounds ------------------------------------------------
+  if (use_p && ystar >= tk) {
+    // Group size: count pass on the exact key (every index in bin 0).
+    pass(24, 0, false, true, ystar);
+    if (tid < 64) {
+      uint64_t c = hist[4 * tid] + hist[4 * tid + 1] + hist[4 * tid + 2] + hist[4 * tid + 3];
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o);
+      if (tid == 0) res_q[3] = c;
+    }
+    __syncthreads();
+    const uint64_t group = res_q[3];
+    __syncthreads();
+    const uint64_t n_keep = keep_of(group);
+    if (n_keep < group)
+      istar = index_bound(n_keep, [&](int shift, uint32_t ipre) { pass(shift, ipre, false, true, ystar); });
   }
   if (tid == 0) a.sel[row] = make_uint4(tk, ystar, istar, 0u);
 }
@@ -977,9 +1097,14 @@ __global__ void __launch_bounds__(kSweepThreads) sample_sweep_kernel(const Accep
 template <typename LT>
 hipError_t launch_sample_t(const AcceptArgs& a, hipStream_t s) {
   const unsigned rows = (unsigned)((int64_t)a.T * a.M);
-  if (a.sel != nullptr) hipLaunchKernelGGL(sample_select_kernel<LT>, dim3(rows), dim3(kSelThreads), 0, s, a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  if (a.sel != nullptr) {
+    hipLaunchKernelGGL(sample_select_kernel<LT>, dim3(rows), dim3(kSelThreads), 0, s, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(sample_radix_kernel<LT>, dim3(rows), dim3(kSelThreads), 0, s, a);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
   hipLaunchKernelGGL(sample_sweep_kernel<LT>, dim3((unsigned)a.nchunk, rows), dim3(kSweepThreads), 0, s, a);
   return hipGetLastError();
 }
