@@ -66,6 +66,31 @@ def test_sample_full_vocab_flat_and_peaked_rows(gpu, sigma, top_p, top_k):
     run_and_compare(lg, a.draft, a.parent_ref, a.pos, 8, 1.0, top_p, top_k, seed=77)
 
 
+def test_sample_random_configurations(gpu):
+    """40 random (dtype, vocabulary, spread, temperature, top-p, top-k, seed)
+    configurations, peaked and flat rows, aligned and unaligned vocabularies:
+    every draw bit-exact against the oracle (the fp32 filters, the head
+    choice, the tail bounds and the radix kernel all take part)."""
+    rng = np.random.default_rng(2026)
+    dts = [torch.bfloat16, torch.float16, torch.float32]
+    for case in range(40):
+        dtype = dts[case % 3]
+        V = int(rng.choice([777, 4099, 8192, 20000, 33333]))
+        sigma = float(rng.choice([0.3, 1.0, 3.0, 8.0]))
+        temperature = float(rng.choice([1.0, 0.5, 0.8, 1.7]))
+        top_p = float(rng.choice([1.0, 0.99, 0.9, 0.6, 0.2]))
+        top_k = int(rng.choice([0, 0, 1, 5, 50, 700]))
+        seed = int(rng.integers(0, 2 ** 63))
+        print(f"[sample random {case}] {dtype} V={V} sigma={sigma} T={temperature} p={top_p} k={top_k}", flush=True)
+        g = torch.Generator().manual_seed(case)
+        lg = (torch.randn((2, 6, V), generator=g) * sigma)
+        if case % 4 == 0:
+            lg[:, :, int(rng.integers(0, V))] += 10.0 * sigma  # a planted favourite
+        lg = lg.to(dtype).to(gpu)
+        a = wl.make_accept_inputs(T=2, M=6, V=V, device=str(gpu), seed=case)
+        run_and_compare(lg, a.draft, a.parent_ref, a.pos, 8, temperature, top_p, top_k, seed)
+
+
 def test_sample_ties_at_the_top_p_cut(gpu):
     """bf16 rows of a few repeated values, so the top-p cut falls inside a tie
     group (kept: its highest indices) and top-k ties are all kept."""
