@@ -271,6 +271,43 @@ def test_tree_verify_batched_paged_f16(gpu, ps):
         assert_lse_close(np64(l_p[b]), l_ref, what=f"b={b}")
 
 
+def test_tree_verify_random_configurations(gpu):
+    """24 random (prefix length, tree size and shape, GQA grouping, head_dim,
+    page size, dtype, bundle packing) configurations: paged and dense cache
+    bit-equal, both within tolerance of the fp64 oracle."""
+    rng = np.random.default_rng(77)
+    for case in range(24):
+        n_prefix = int(rng.choice([0, 1, 33, 1000, 9000]))
+        M = int(rng.choice([1, 7, 33, 64, 100, 200, 256]))
+        H, Hk = [(8, 8), (32, 8), (16, 4), (8, 2), (4, 1)][case % 5]
+        D = int(rng.choice([64, 128]))
+        ps = int(rng.choice([1, 16, 64]))
+        dtype = torch.float16 if case % 3 == 0 else torch.bfloat16
+        depth, outdeg = int(rng.integers(1, 13)), int(rng.integers(1, 7))
+        # A tree of depth <= d and out-degree <= o holds at most 1 + o + ... + o^d nodes.
+        while sum(outdeg ** k for k in range(depth + 1)) < M:
+            depth, outdeg = depth + 1, min(outdeg + 1, 6)
+        print(f"[tree_verify random {case}] N={n_prefix} M={M} H={H}/{Hk} D={D} ps={ps} {dtype} "
+              f"depth={depth} outdeg={outdeg}", flush=True)
+        inp = wl.make_tree_verify_inputs(n_prefix=n_prefix, M=M, H=H, Hk=Hk, D=D, page_size=ps, dtype=dtype,
+                                         seed=100 + case, tree_seed=200 + case, max_depth=depth, max_outdeg=outdeg,
+                                         device=str(gpu))
+        par = torch.tensor(inp.parent, dtype=torch.int64, device=gpu)
+        perm = None
+        if case % 2 == 1:
+            perm = torch.tensor(bundle_row_order(inp.parent, num_bundles=int(rng.integers(1, 9))), dtype=torch.int32,
+                                device=gpu)
+        o_p, l_p = tree_verify(inp.q, inp.kv_pages[0, 0], inp.kv_pages[0, 1], n_prefix, par,
+                               page_table=inp.page_table, row_perm=perm)
+        kc, vc = inp.logical_kv(0, 0).contiguous(), inp.logical_kv(0, 1).contiguous()
+        o_d, l_d = tree_verify(inp.q, kc, vc, n_prefix, par, row_perm=perm)
+        torch.cuda.synchronize()
+        assert torch.equal(o_p, o_d) and torch.equal(l_p, l_d), f"case {case}: paged differs from dense"
+        o_ref, l_ref = oracle_tree_verify(inp)
+        assert_attn_close(np64(o_p[0]), o_ref, what=f"case {case}")
+        assert_lse_close(np64(l_p[0]), l_ref, what=f"case {case}")
+
+
 def test_tree_verify_dense_equals_paged_and_perm_invariant(gpu):
     inp = paged_case(gpu, 3000, 64, tree_seed=5)
     par = torch.tensor(inp.parent, dtype=torch.int32, device=gpu)
