@@ -39,10 +39,12 @@
 //       passes over the row and the sweep draws.
 //   sample_sweep_kernel   one workgroup per (row, vocabulary range) of the
 //       rows still open (all rows without top-p / top-k):
-//       the Gumbel-max draw over the range's kept entries.  An fp32 estimate
-//       of each z (within 2^-14 of it) against a wave-shared lower bound of
-//       the range's maximum z leaves the exact double evaluation to the few
-//       entries that can still win.
+//       the Gumbel-max draw over the range's kept entries.  Against a
+//       wave-shared lower bound lb of the range's maximum z, an entry whose
+//       1 - U exceeds an upper bound of e^(y - lb) cannot reach lb (one 2^x
+//       per entry from x * fl(1/T)); the few others take the exact warper,
+//       the keep test and an fp32 estimate of z (within 2^-14 of it), which
+//       leaves the exact double evaluation to the entries that can still win.
 //   the walk of dsv_accept.hip combines the ranges' draws and walks.
 
 #include "dsv_internal.h"
@@ -216,10 +218,13 @@ __device__ __forceinline__ float round_lt(float y) {
 // y of one logit: x / T (IEEE division, correctly rounded by default in HIP)
 // rounded to the logits dtype (T == 1: x); NaN -> -inf, -0 -> +0.
 template <typename LT>
-__device__ __forceinline__ float warp_y(LT raw, const Warp& w) {
-  float y = raw_to_f<LT>(raw);
+__device__ __forceinline__ float warp_yf(float y, const Warp& w) {
   if (w.T != 1.f) y = round_lt<LT>(y / w.T);
   return clean_y(y);
+}
+template <typename LT>
+__device__ __forceinline__ float warp_y(LT raw, const Warp& w) {
+  return warp_yf<LT>(raw_to_f<LT>(raw), w);
 }
 
 // warp_y of N values held as floats.  For 16-bit logits q = x * fl(1/T) lies
@@ -276,11 +281,10 @@ __device__ __forceinline__ uint32_t ykey(float y) {
   return b ^ ((b >> 31) ? 0xFFFFFFFFu : 0x80000000u);
 }
 
-// y of N = 16 / sizeof(LT) consecutive logits from v0 (entries at or past hi
-// read as -inf): one 16-byte load when the row is 16-byte aligned.
-template <typename LT, bool WARP>
-__device__ __forceinline__ void load_y(const LT* x, int64_t v0, int64_t hi, bool aligned, const Warp& T,
-                                       float (&y)[16 / sizeof(LT)]) {
+// N = 16 / sizeof(LT) consecutive logits from v0 as floats (entries at or
+// past hi read as -inf): one 16-byte load when the row is 16-byte aligned.
+template <typename LT>
+__device__ __forceinline__ void load_x(const LT* x, int64_t v0, int64_t hi, bool aligned, float (&y)[16 / sizeof(LT)]) {
   constexpr int N = 16 / sizeof(LT);
   if (aligned && v0 + N <= hi) {
     const u32x4 r = *reinterpret_cast<const u32x4*>(x + v0);
@@ -297,6 +301,15 @@ __device__ __forceinline__ void load_y(const LT* x, int64_t v0, int64_t hi, bool
 #pragma unroll
     for (int e = 0; e < N; ++e) y[e] = v0 + e < hi ? raw_to_f<LT>(x[v0 + e]) : kNegInfF;
   }
+}
+
+// y of N = 16 / sizeof(LT) consecutive logits from v0 (entries at or past hi
+// read as -inf).
+template <typename LT, bool WARP>
+__device__ __forceinline__ void load_y(const LT* x, int64_t v0, int64_t hi, bool aligned, const Warp& T,
+                                       float (&y)[16 / sizeof(LT)]) {
+  constexpr int N = 16 / sizeof(LT);
+  load_x<LT>(x, v0, hi, aligned, y);
   if constexpr (WARP) {
     warp_vec<LT, N>(y, T);
   } else {
@@ -309,8 +322,8 @@ __device__ __forceinline__ void load_y(const LT* x, int64_t v0, int64_t hi, bool
 // the threads of a block take consecutive vectors, two vectors per thread and
 // iteration with both loads in flight.  Every lane of a wave runs the same
 // iterations, so f may use wave ballots and shuffles.  WARP = false hands f
-// the logits themselves (NaN as -inf).
-template <typename LT, int NT, bool WARP = true, typename F>
+// the logits themselves (NaN as -inf), RAW = true the logits as loaded.
+template <typename LT, int NT, bool WARP = true, bool RAW = false, typename F>
 __device__ __forceinline__ void row_sweep(const LT* x, int64_t lo, int64_t hi, const Warp& T, F&& f) {
   constexpr int N = 16 / sizeof(LT);
   const bool aligned = (reinterpret_cast<uintptr_t>(x) & 15) == 0;
@@ -318,8 +331,13 @@ __device__ __forceinline__ void row_sweep(const LT* x, int64_t lo, int64_t hi, c
   for (int64_t b0 = lo + (int64_t)(threadIdx.x & ~63) * N; b0 < hi; b0 += (int64_t)2 * NT * N) {
     const int64_t v0 = b0 + (int64_t)lane * N, v1 = v0 + (int64_t)NT * N;
     float ya[N], yb[N];
-    load_y<LT, WARP>(x, v0, hi, aligned, T, ya);
-    load_y<LT, WARP>(x, v1, hi, aligned, T, yb);
+    if constexpr (RAW) {
+      load_x<LT>(x, v0, hi, aligned, ya);
+      load_x<LT>(x, v1, hi, aligned, yb);
+    } else {
+      load_y<LT, WARP>(x, v0, hi, aligned, T, ya);
+      load_y<LT, WARP>(x, v1, hi, aligned, T, yb);
+    }
     f(v0, ya);
     f(v1, yb);
   }
@@ -1039,50 +1057,70 @@ __global__ void __launch_bounds__(kSweepThreads) sample_sweep_kernel(const Accep
   int bi = -1;
   float lb = kNegInfF;   // wave-uniform lower bound of the range's maximum z
   float lbl = kNegInfF;  // this lane's share of it
+  // ya = x * fl(1/T) is within 2^-8 |ya| + 2^-25 of y (the division rounded to
+  // the logits dtype; y = x when T == 1); yh = ya + 2^-7 |ya| bounds y from
+  // above, up to 2^-25.
+  const float rT = wp.T != 1.f ? wp.rT : 1.f;
   // Every lane of a wave runs the same iterations (the bound is shared by
   // shuffles); a vector of NV entries is NV / 4 generator groups.
   constexpr int NV = 16 / sizeof(LT);
-  row_sweep<LT, kSweepThreads>(x, lo, hi, wp, [&](int64_t v0, const float(&yv)[NV]) {
+  row_sweep<LT, kSweepThreads, false, true>(x, lo, hi, wp, [&](int64_t v0, const float(&xv)[NV]) {
+    bool upd = false;
 #pragma unroll
     for (int gq = 0; gq < NV / 4; ++gq) {
       const int64_t g = v0 + 4 * gq;
-      bool kp[4];
+      float yh[4];
       float ym = kNegInfF;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float yy = yv[4 * gq + e];
-        const uint32_t k = ykey(yy);
-        kp[e] = yy > kNegInfF && k >= tk && (k > ystar || (k == ystar && (uint32_t)(g + e) >= istar));
-        if (kp[e]) ym = fmaxf(ym, yy);
+        const float ya = xv[4 * gq + e] * rT;
+        float h = fmaf(fabsf(ya), 0x1p-7f, ya);  // NaN for x = -inf or NaN: such entries are screened exactly
+        // f16: a quotient at or above 65520 rounds to +inf.
+        if constexpr (__is_same(LT, _Float16)) h = h >= 65520.f ? __builtin_huge_valf() : h;
+        yh[e] = h;
+        ym = fmaxf(ym, h);
       }
-      // G < kGumbelMax: a group whose largest kept y cannot reach the bound
-      // holds no winner and needs no generator call.
-      if (ym > kNegInfF && ym + kGumbelMax + kZMargin + (fabsf(ym) + kGumbelMax) * kZMarginRel >= lb) {
-        const uint4 w4 = philox4x32((uint32_t)(g >> 2), (uint32_t)i, (uint32_t)t, 0u, k0, k1);
+      // G < kGumbelMax: a group whose largest y cannot reach the bound holds
+      // no winner and needs no generator call.
+      if (!(ym + kGumbelMax >= lb)) continue;
+      const uint4 w4 = philox4x32((uint32_t)(g >> 2), (uint32_t)i, (uint32_t)t, 0u, k0, k1);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          if (!kp[e]) continue;
-          const float yy = yv[4 * gq + e];
-          const uint32_t w = word_of(w4, e);
-          const float zf = yy + gumbel_est(w);
-          const float mg = kZMargin + fabsf(zf) * kZMarginRel;
-          lbl = fmaxf(lbl, zf - mg);
-          if (zf + mg >= lb) {
-            // Within the margin of the bound: the exact draw (entries of a
-            // lane come in increasing index, so a tie keeps the first).
-            const double z = (double)yy + gumbel(w);
-            if (bi < 0 || z > best) {
-              best = z;
-              bi = (int)(g + e);
-            }
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t w = word_of(w4, e);
+        // Screen: 1 - U <= -ln U, so 1 - U > e^(y - lb) gives
+        // G = -ln(-ln U) < lb - y, i.e. z < lb: not the maximum.  Both sides
+        // are scaled by 2^32: ~w (rounded to fp32, within 2^-24 of it) is at
+        // most 2^32 (1 - U) = ~w + 1/2, and tq is at least 2^32 e^(y - lb)
+        // (an exponent margin of 2^-9 covers y's 2^-25, the rounding of the
+        // argument for every |yh - lb| where 2^x neither overflows nor
+        // underflows, and the hardware 2^x).  NaN passes.
+        const float tq = __builtin_amdgcn_exp2f(fmaf(yh[e] - lb, 0x1.715476p+0f, 32.f + 0x1p-9f));
+        if ((float)(~w) > tq) continue;
+        // The exact y and the keep test, then the fp32 estimate of z.
+        const float yy = warp_yf<LT>(xv[4 * gq + e], wp);
+        const uint32_t k = ykey(yy);
+        if (!(yy > kNegInfF && k >= tk && (k > ystar || (k == ystar && (uint32_t)(g + e) >= istar)))) continue;
+        const float zf = yy + gumbel_est(w);
+        const float mg = kZMargin + fabsf(zf) * kZMarginRel;
+        lbl = fmaxf(lbl, zf - mg);
+        upd = true;
+        if (zf + mg >= lb) {
+          // Within the margin of the bound: the exact draw (entries of a
+          // lane come in increasing index, so a tie keeps the first).
+          const double z = (double)yy + gumbel(w);
+          if (bi < 0 || z > best) {
+            best = z;
+            bi = (int)(g + e);
           }
         }
       }
     }
-    float wl = lbl;
+    if (__ballot(upd) != 0ull) {
+      float wl = lbl;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) wl = fmaxf(wl, __shfl_xor(wl, o));
-    lb = wl;
+      for (int o = 32; o > 0; o >>= 1) wl = fmaxf(wl, __shfl_xor(wl, o));
+      lb = wl;
+    }
   });
   __shared__ double sb[kSweepThreads / 64];
   __shared__ int si[kSweepThreads / 64];
