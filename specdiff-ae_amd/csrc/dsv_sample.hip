@@ -281,13 +281,21 @@ __device__ __forceinline__ uint32_t ykey(float y) {
   return b ^ ((b >> 31) ? 0xFFFFFFFFu : 0x80000000u);
 }
 
-// N = 16 / sizeof(LT) consecutive logits from v0 as floats (entries at or
-// past hi read as -inf): one 16-byte load when the row is 16-byte aligned.
+// The 16-byte vector of logits at v0 when it is whole and the row is 16-byte
+// aligned (otherwise zero: unpack_vec then reads the entries one by one).
 template <typename LT>
-__device__ __forceinline__ void load_x(const LT* x, int64_t v0, int64_t hi, bool aligned, float (&y)[16 / sizeof(LT)]) {
+__device__ __forceinline__ u32x4 fetch_vec(const LT* x, int64_t v0, int64_t hi, bool aligned) {
+  constexpr int N = 16 / sizeof(LT);
+  return (aligned && v0 + N <= hi) ? *reinterpret_cast<const u32x4*>(x + v0) : u32x4{0, 0, 0, 0};
+}
+
+// N = 16 / sizeof(LT) consecutive logits from v0 as floats (entries at or
+// past hi read as -inf), from fetch_vec's vector r.
+template <typename LT>
+__device__ __forceinline__ void unpack_vec(const LT* x, int64_t v0, int64_t hi, bool aligned, const u32x4& r,
+                                           float (&y)[16 / sizeof(LT)]) {
   constexpr int N = 16 / sizeof(LT);
   if (aligned && v0 + N <= hi) {
-    const u32x4 r = *reinterpret_cast<const u32x4*>(x + v0);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       if constexpr (sizeof(LT) == 4) {
@@ -303,13 +311,9 @@ __device__ __forceinline__ void load_x(const LT* x, int64_t v0, int64_t hi, bool
   }
 }
 
-// y of N = 16 / sizeof(LT) consecutive logits from v0 (entries at or past hi
-// read as -inf).
-template <typename LT, bool WARP>
-__device__ __forceinline__ void load_y(const LT* x, int64_t v0, int64_t hi, bool aligned, const Warp& T,
-                                       float (&y)[16 / sizeof(LT)]) {
-  constexpr int N = 16 / sizeof(LT);
-  load_x<LT>(x, v0, hi, aligned, y);
+// y of loaded logits: the warper (WARP) or NaN -> -inf and -0 -> +0 only.
+template <typename LT, bool WARP, int N>
+__device__ __forceinline__ void finish_y(float (&y)[N], const Warp& T) {
   if constexpr (WARP) {
     warp_vec<LT, N>(y, T);
   } else {
@@ -320,26 +324,39 @@ __device__ __forceinline__ void load_y(const LT* x, int64_t v0, int64_t hi, bool
 
 // Runs f(v0, y) over [lo, hi) in vectors of N entries (lo a multiple of N):
 // the threads of a block take consecutive vectors, two vectors per thread and
-// iteration with both loads in flight.  Every lane of a wave runs the same
-// iterations, so f may use wave ballots and shuffles.  WARP = false hands f
-// the logits themselves (NaN as -inf), RAW = true the logits as loaded.
+// iteration, and the next iteration's two loads are issued before f runs on
+// this one's, so that a thread keeps up to four vector loads in flight.
+// Every lane of a wave runs the same iterations, so f may use wave ballots
+// and shuffles.  WARP = false hands f the logits themselves (NaN as -inf),
+// RAW = true the logits as loaded.
 template <typename LT, int NT, bool WARP = true, bool RAW = false, typename F>
 __device__ __forceinline__ void row_sweep(const LT* x, int64_t lo, int64_t hi, const Warp& T, F&& f) {
   constexpr int N = 16 / sizeof(LT);
+  constexpr int64_t kStep = (int64_t)2 * NT * N;
   const bool aligned = (reinterpret_cast<uintptr_t>(x) & 15) == 0;
   const int lane = threadIdx.x & 63;
-  for (int64_t b0 = lo + (int64_t)(threadIdx.x & ~63) * N; b0 < hi; b0 += (int64_t)2 * NT * N) {
+  int64_t b0 = lo + (int64_t)(threadIdx.x & ~63) * N;  // uniform over the wave
+  if (b0 >= hi) return;
+  u32x4 ra = fetch_vec<LT>(x, b0 + (int64_t)lane * N, hi, aligned);
+  u32x4 rb = fetch_vec<LT>(x, b0 + (int64_t)lane * N + (int64_t)NT * N, hi, aligned);
+  for (; b0 < hi; b0 += kStep) {
     const int64_t v0 = b0 + (int64_t)lane * N, v1 = v0 + (int64_t)NT * N;
+    u32x4 na = u32x4{0, 0, 0, 0}, nb = u32x4{0, 0, 0, 0};
+    if (b0 + kStep < hi) {
+      na = fetch_vec<LT>(x, v0 + kStep, hi, aligned);
+      nb = fetch_vec<LT>(x, v1 + kStep, hi, aligned);
+    }
     float ya[N], yb[N];
-    if constexpr (RAW) {
-      load_x<LT>(x, v0, hi, aligned, ya);
-      load_x<LT>(x, v1, hi, aligned, yb);
-    } else {
-      load_y<LT, WARP>(x, v0, hi, aligned, T, ya);
-      load_y<LT, WARP>(x, v1, hi, aligned, T, yb);
+    unpack_vec<LT>(x, v0, hi, aligned, ra, ya);
+    unpack_vec<LT>(x, v1, hi, aligned, rb, yb);
+    if constexpr (!RAW) {
+      finish_y<LT, WARP>(ya, T);
+      finish_y<LT, WARP>(yb, T);
     }
     f(v0, ya);
     f(v1, yb);
+    ra = na;
+    rb = nb;
   }
 }
 
