@@ -160,7 +160,8 @@ def fixed_masses(y: np.ndarray) -> np.ndarray:
     m = y.max()
     if not np.isfinite(m) and m < 0:
         return np.zeros(V, dtype=U64)
-    d = np.where(y == m, 0.0, y - m)
+    with np.errstate(invalid="ignore"):  # m = +inf: inf - inf where y == m, replaced by 0
+        d = np.where(y == m, 0.0, y - m)
     p = det_exp2(d * LOG2E)
     return np.rint(np.ldexp(p, S)).astype(U64)
 

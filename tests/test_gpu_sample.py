@@ -111,6 +111,32 @@ def test_sample_ties_at_the_top_p_cut(gpu):
     assert r["next"][0, 3].item() == 17 and r["next"][0, 4].item() == 0
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_sample_rows_with_infinite_logits(gpu, dtype):
+    """Rows holding +inf logits (one, two tied, with NaNs beside), and f16 rows
+    whose warped values overflow to +inf at temperature 0.7: every +inf entry
+    has the maximum's mass, the others none; ties drawn by the lowest index."""
+    M, V = 6, 4099
+    g = torch.Generator().manual_seed(8)
+    lg = torch.randint(-3, 3, (1, M, V), generator=g).float()
+    lg[0, 1, 50] = float("inf")
+    lg[0, 2, 60] = float("inf")
+    lg[0, 2, 70] = float("inf")
+    lg[0, 3, 80] = float("inf")
+    lg[0, 3, 90:95] = float("nan")
+    lg[0, 4, 1000] = 50000.0                        # f16: 50000 / 0.7 rounds to +inf
+    lg[0, 4, 2000] = 60000.0
+    lg[0, 5, 3000] = 40000.0                        # f16: 40000 / 0.7 = 57142.9 stays finite
+    lg = lg.to(dtype)
+    draft = torch.randint(0, V, (1, M), generator=g)
+    parent_ref = torch.tensor([[-1, 0, 1, 2, 3]])
+    pos = torch.arange(M)
+    for temperature, top_p, top_k in [(1.0, 1.0, 0), (0.7, 1.0, 0), (0.7, 0.9, 0), (1.0, 1.0, 5), (1.3, 0.5, 7)]:
+        print(f"[sample inf] {dtype} T={temperature} top_p={top_p} top_k={top_k}", flush=True)
+        run_and_compare(lg.to(gpu), draft.to(gpu), parent_ref.to(gpu), pos.to(gpu), 8, temperature, top_p, top_k,
+                        seed=31)
+
+
 @pytest.mark.parametrize("temperature,top_p,top_k", [(1.0, 1.0, 0), (0.6, 0.85, 0), (1.5, 1.0, 6)])
 def test_sample_frequencies_follow_the_warped_softmax(gpu, temperature, top_p, top_k):
     """4096 draws of one 24-token row (512 trees x 8 nodes with the same logits)."""
