@@ -794,6 +794,7 @@ static bool stream16_ok(const AcceptArgs& a) {
 }
 
 void accept_chunking(AcceptArgs& a, int cus) {
+  a.cus = cus;
   if (stream16_ok(a)) {
     const int64_t rows = (int64_t)a.T * a.M, nsub = (a.V + kSub - 1) / kSub;
     const int64_t want = std::max<int64_t>(1, (4 * (int64_t)cus + rows - 1) / rows);

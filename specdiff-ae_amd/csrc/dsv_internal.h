@@ -131,6 +131,7 @@ struct AcceptArgs {
   int64_t top_k;           // 0: no top-k
   uint64_t seed;           // Philox key word 0
   uint4* sel;              // [T*M] kept-set bounds (top-k key, top-p key, top-p index); nullptr: keep all
+  int cus;                 // compute units of the device (launch shapes); set by accept_chunking
 };
 
 // Arguments of the accepted-path KV commit.

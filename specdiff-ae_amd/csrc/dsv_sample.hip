@@ -53,11 +53,10 @@ namespace dsv {
 
 namespace {
 
-constexpr int kSelThreads = 1024;
+constexpr int kRadixThreads = 1024;
 constexpr int kSweepThreads = 256;
 constexpr float kNegInfF = -__builtin_huge_valf();
 constexpr int kCap = 4096;   // candidates the select kernel's fast path sorts in LDS
-static_assert(kCap % kSelThreads == 0, "candidates split evenly over the threads");
 // Ladder of candidate thresholds m - y <= theta_j: the floats whose bits are
 // (250 + j) << 22, i.e. 2^e and 1.5 * 2^e from 1/4 to 48.
 constexpr int kNTheta = 16;
@@ -462,8 +461,9 @@ __device__ __forceinline__ int scan_desc(const uint64_t* w, uint64_t target, uin
   return __shfl(found, first);
 }
 
-template <typename LT>
-__global__ void __launch_bounds__(kSelThreads) sample_select_kernel(const AcceptArgs a) {
+template <typename LT, int NT>
+__global__ void __launch_bounds__(NT) sample_select_kernel(const AcceptArgs a) {
+  static_assert(kCap % NT == 0, "candidates split evenly over the threads");
   const int64_t row = blockIdx.x;
   const int t = (int)(row / a.M), i = (int)(row % a.M);
   const LT* x = reinterpret_cast<const LT*>(a.logits) + (int64_t)t * a.l_st + (int64_t)i * a.l_sm;
@@ -472,13 +472,13 @@ __global__ void __launch_bounds__(kSelThreads) sample_select_kernel(const Accept
   constexpr int ND = key_digits<LT>();
   const Warp wp = make_warp(a.temperature);
 
-  __shared__ float red_f[kSelThreads / 64];
+  __shared__ float red_f[NT / 64];
 
   // Row maximum of y: the warper is monotone, so it is the warped maximum
   // logit (xm).
   float m = kNegInfF;
   constexpr int NV = 16 / sizeof(LT);
-  row_sweep<LT, kSelThreads, false>(x, 0, V, wp, [&](int64_t, const float(&y)[NV]) {
+  row_sweep<LT, NT, false>(x, 0, V, wp, [&](int64_t, const float(&y)[NV]) {
 #pragma unroll
     for (int e = 0; e < NV; ++e) m = fmaxf(m, y[e]);
   });
@@ -488,7 +488,7 @@ __global__ void __launch_bounds__(kSelThreads) sample_select_kernel(const Accept
   __syncthreads();
   if (tid == 0) {
     float mm = red_f[0];
-    for (int w = 1; w < kSelThreads / 64; ++w) mm = fmaxf(mm, red_f[w]);
+    for (int w = 1; w < NT / 64; ++w) mm = fmaxf(mm, red_f[w]);
     red_f[0] = mm;
   }
   __syncthreads();
@@ -526,10 +526,10 @@ __global__ void __launch_bounds__(kSelThreads) sample_select_kernel(const Accept
   __shared__ uint32_t ncand, nk_lo, nk_hi;
   __shared__ int jsel[2];
   __shared__ uint32_t n_eq;
-  __shared__ float red_l[kSelThreads / 64];
-  __shared__ uint64_t red_q[kSelThreads / 64];
-  __shared__ double red_d[kSelThreads / 64];
-  __shared__ int red_i[kSelThreads / 64];
+  __shared__ float red_l[NT / 64];
+  __shared__ uint64_t red_q[NT / 64];
+  __shared__ double red_d[NT / 64];
+  __shared__ int red_i[NT / 64];
 
   if (tid < kNTheta) cnt_th[tid] = 0;
   if (tid == 0) {
@@ -561,7 +561,7 @@ __global__ void __launch_bounds__(kSelThreads) sample_select_kernel(const Accept
       pk0 = 0;
       pk1 = 0;
     };
-    row_sweep<LT, kSelThreads, false>(x, 0, V, wp, [&](int64_t, const float(&y)[NV]) {
+    row_sweep<LT, NT, false>(x, 0, V, wp, [&](int64_t, const float(&y)[NV]) {
 #pragma unroll
       for (int e = 0; e < NV; ++e) {
         const float d = (xm - y[e]) * wp.rT;
@@ -609,7 +609,7 @@ __global__ void __launch_bounds__(kSelThreads) sample_select_kernel(const Accept
     int j0 = -1, j1 = -1;
     if (use_p) {
       float L = 0.f;
-      for (int w = 0; w < kSelThreads / 64; ++w) L += red_l[w];
+      for (int w = 0; w < NT / 64; ++w) L += red_l[w];
       const float need = (float)a.top_p_q * 0x1p-32f * L * (1.f + 0x1p-8f);
       float head = (float)n_eq + (float)(cnt_th[0] - n_eq) * __expf(-kTheta[0]);
       for (int j = 0; j < kNTheta && cnt_th[j] <= (uint32_t)kCap; ++j) {
@@ -641,7 +641,7 @@ __global__ void __launch_bounds__(kSelThreads) sample_select_kernel(const Accept
     const float ts = kTheta[jsel[att]];
     // Gather the candidates; sum the fp32 masses of the others.
     float tail = 0.f;
-    row_sweep<LT, kSelThreads>(x, 0, V, wp, [&](int64_t v0, const float(&y)[NV]) {
+    row_sweep<LT, NT>(x, 0, V, wp, [&](int64_t v0, const float(&y)[NV]) {
       bool any = false;
 #pragma unroll
       for (int e = 0; e < NV; ++e) {
@@ -674,15 +674,15 @@ __global__ void __launch_bounds__(kSelThreads) sample_select_kernel(const Accept
     // the gathered count decides whether the head fits and holds k entries.
     const bool fits = (int)ncand <= kCap && (use_p || (int64_t)ncand >= kk);
     float tail_all = 0.f;
-    for (int w = 0; w < kSelThreads / 64; ++w) tail_all += red_f[w];
+    for (int w = 0; w < NT / 64; ++w) tail_all += red_f[w];
     // Bitonic sort, descending, padded with zero keys to a power of two.
     int npad = 2;
     while (npad < n) npad <<= 1;
-    for (int q = n + tid; q < npad; q += kSelThreads) cand[q] = 0ull;
+    for (int q = n + tid; q < npad; q += NT) cand[q] = 0ull;
     __syncthreads();
     for (int k2 = 2; k2 <= npad; k2 <<= 1)
       for (int j2 = k2 >> 1; j2 > 0; j2 >>= 1) {
-        for (int q = tid; q < npad; q += kSelThreads) {
+        for (int q = tid; q < npad; q += NT) {
           const int l = q ^ j2;
           if (l > q) {
             const uint64_t u = cand[q], w = cand[l];
@@ -702,7 +702,7 @@ __global__ void __launch_bounds__(kSelThreads) sample_select_kernel(const Accept
     if (use_p && ok) {
       // Exact masses along the order (thread tid holds entries EPT * tid ..
       // + EPT - 1) and their exclusive prefix sums.
-      constexpr int EPT = kCap / kSelThreads;
+      constexpr int EPT = kCap / NT;
       uint64_t qv[EPT], tot = 0;
 #pragma unroll
       for (int u = 0; u < EPT; ++u) {
@@ -719,7 +719,7 @@ __global__ void __launch_bounds__(kSelThreads) sample_select_kernel(const Accept
       if (lane == 63) red_q[wv] = incl;
       __syncthreads();
       uint64_t wbase = 0, H = 0;
-      for (int w = 0; w < kSelThreads / 64; ++w) {
+      for (int w = 0; w < NT / 64; ++w) {
         if (w < wv) wbase += red_q[w];
         H += red_q[w];
       }
@@ -757,7 +757,7 @@ __global__ void __launch_bounds__(kSelThreads) sample_select_kernel(const Accept
     if (ok) {
       double bz = -__builtin_huge_val();
       int bi = -1;
-      for (int q = tid; q < n; q += kSelThreads) {
+      for (int q = tid; q < n; q += NT) {
         const uint64_t cv = cand[q];
         const uint32_t key = (uint32_t)(cv >> 32);
         const int v = (int)(uint32_t)cv;
@@ -769,7 +769,7 @@ __global__ void __launch_bounds__(kSelThreads) sample_select_kernel(const Accept
           }
         }
       }
-      block_argmax(bz, bi, red_d, red_i, kSelThreads);
+      block_argmax(bz, bi, red_d, red_i, NT);
       if (tid == 0) finish(bz, bi);
       return;
     }
@@ -785,7 +785,7 @@ __global__ void __launch_bounds__(kSelThreads) sample_select_kernel(const Accept
 // the kept set is then gathered and drawn here when it fits in LDS, else the
 // bounds go to the sweep kernel.
 template <typename LT>
-__global__ void __launch_bounds__(kSelThreads) sample_radix_kernel(const AcceptArgs a) {
+__global__ void __launch_bounds__(kRadixThreads) sample_radix_kernel(const AcceptArgs a) {
   const int64_t row = blockIdx.x;
   const uint4 st = a.sel[row];
   if (st.w != 2u) return;
@@ -809,8 +809,8 @@ __global__ void __launch_bounds__(kSelThreads) sample_radix_kernel(const AcceptA
   __shared__ uint64_t res_q[4];
   __shared__ uint64_t cand[kCap];
   __shared__ uint32_t ncand, nk_lo;
-  __shared__ double red_d[kSelThreads / 64];
-  __shared__ int red_i[kSelThreads / 64];
+  __shared__ double red_d[kRadixThreads / 64];
+  __shared__ int red_i[kRadixThreads / 64];
   auto finish = [&](double z, int idx) {
     const uint64_t zb = __builtin_bit_cast(uint64_t, z);
     for (int c = 0; c < a.nchunk; ++c)
@@ -829,7 +829,7 @@ __global__ void __launch_bounds__(kSelThreads) sample_radix_kernel(const AcceptA
     if (tid < 256) hist[tid] = 0;
     __syncthreads();
     const uint32_t hi_mask = shift >= 24 ? 0u : ~((1u << (shift + 8)) - 1u);
-    row_sweep<LT, kSelThreads>(x, 0, V, wp, [&](int64_t v0, const float(&y)[NV]) {
+    row_sweep<LT, kRadixThreads>(x, 0, V, wp, [&](int64_t v0, const float(&y)[NV]) {
 #pragma unroll
       for (int e = 0; e < NV; ++e) {
         const uint32_t k = ykey(y[e]);
@@ -963,7 +963,7 @@ __global__ void __launch_bounds__(kSelThreads) sample_radix_kernel(const AcceptA
     constexpr int kList = 2 * kCap;
     if (tid == 0) ncand = 0;
     __syncthreads();
-    row_sweep<LT, kSelThreads>(x, 0, V, wp, [&](int64_t v0, const float(&y)[NV]) {
+    row_sweep<LT, kRadixThreads>(x, 0, V, wp, [&](int64_t v0, const float(&y)[NV]) {
       bool any = false;
 #pragma unroll
       for (int e = 0; e < NV; ++e) any |= v0 + e < V && ykey(y[e]) >= lower;
@@ -989,7 +989,7 @@ __global__ void __launch_bounds__(kSelThreads) sample_radix_kernel(const AcceptA
       auto key_at = [&](int q) { return ykey(warp_y<LT>(x[list[q]], wp)); };
       if (use_p && ystar >= tk) {
         uint32_t g = 0;
-        for (int q = tid; q < nl; q += kSelThreads) g += key_at(q) == ystar ? 1u : 0u;
+        for (int q = tid; q < nl; q += kRadixThreads) g += key_at(q) == ystar ? 1u : 0u;
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) g += __shfl_xor(g, o);
         if (tid == 0) nk_lo = 0;
@@ -1003,7 +1003,7 @@ __global__ void __launch_bounds__(kSelThreads) sample_radix_kernel(const AcceptA
             if (tid < 256) hist[tid] = 0;
             __syncthreads();
             const uint32_t hi_mask = shift >= 24 ? 0u : ~((1u << (shift + 8)) - 1u);
-            for (int q = tid; q < nl; q += kSelThreads) {
+            for (int q = tid; q < nl; q += kRadixThreads) {
               const uint32_t v = list[q];
               if (key_at(q) == ystar && (v & hi_mask) == (ipre & hi_mask))
                 atomicAdd(reinterpret_cast<unsigned long long*>(&hist[(v >> shift) & 255u]), 1ull);
@@ -1013,7 +1013,7 @@ __global__ void __launch_bounds__(kSelThreads) sample_radix_kernel(const AcceptA
       }
       double bz = -__builtin_huge_val();
       int bi = -1;
-      for (int q = tid; q < nl; q += kSelThreads) {
+      for (int q = tid; q < nl; q += kRadixThreads) {
         const int v = (int)list[q];
         const float y = warp_y<LT>(x[v], wp);
         const uint32_t k = ykey(y);
@@ -1025,7 +1025,7 @@ __global__ void __launch_bounds__(kSelThreads) sample_radix_kernel(const AcceptA
           }
         }
       }
-      block_argmax(bz, bi, red_d, red_i, kSelThreads);
+      block_argmax(bz, bi, red_d, red_i, kRadixThreads);
       if (tid == 0) finish(bz, bi);
       return;
     }
@@ -1153,10 +1153,15 @@ template <typename LT>
 hipError_t launch_sample_t(const AcceptArgs& a, hipStream_t s) {
   const unsigned rows = (unsigned)((int64_t)a.T * a.M);
   if (a.sel != nullptr) {
-    hipLaunchKernelGGL(sample_select_kernel<LT>, dim3(rows), dim3(kSelThreads), 0, s, a);
+    // One workgroup per row: 1024 threads when the rows leave CUs idle, else
+    // 512, so that each CU holds two rows and their serial phases overlap.
+    if ((int64_t)rows >= 2 * (int64_t)(a.cus > 0 ? a.cus : 256))
+      hipLaunchKernelGGL((sample_select_kernel<LT, 512>), dim3(rows), dim3(512), 0, s, a);
+    else
+      hipLaunchKernelGGL((sample_select_kernel<LT, 1024>), dim3(rows), dim3(1024), 0, s, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(sample_radix_kernel<LT>, dim3(rows), dim3(kSelThreads), 0, s, a);
+    hipLaunchKernelGGL(sample_radix_kernel<LT>, dim3(rows), dim3(kRadixThreads), 0, s, a);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }

@@ -52,6 +52,17 @@ def test_sample_full_vocab_64_nodes(gpu):
     run_and_compare(a.logits, a.draft, a.parent_ref, a.pos, 8, 1.0, 1.0, 0, seed=7)
 
 
+def test_sample_many_rows(gpu):
+    """8 trees x 64 nodes = 512 rows, at least two per CU: the select kernel
+    runs its 512-thread workgroups (fewer rows take 1024 threads)."""
+    a = wl.make_accept_inputs(T=8, M=64, V=8192 + 3, device=str(gpu), seed=31)
+    run_and_compare(a.logits, a.draft, a.parent_ref, a.pos, 8, 0.7, 0.9, 50, seed=77)
+    run_and_compare(a.logits, a.draft, a.parent_ref, a.pos, 8, 1.0, 0.8, 0, seed=78)
+    flat = (torch.randn((8, 64, 8192 + 3), generator=torch.Generator().manual_seed(3)) * 0.5).to(torch.bfloat16)
+    run_and_compare(flat.to(gpu), a.draft, a.parent_ref, a.pos, 8, 1.0, 0.9, 0, seed=79)
+    run_and_compare(flat.to(gpu), a.draft, a.parent_ref, a.pos, 8, 1.0, 1.0, 100, seed=80)
+
+
 @pytest.mark.parametrize("sigma,top_p,top_k", [(0.3, 0.9, 0), (0.3, 1.0, 3000), (3.0, 1.0, 2000), (3.0, 0.999, 0),
                                              (3.0, 0.5, 7)])
 def test_sample_full_vocab_flat_and_peaked_rows(gpu, sigma, top_p, top_k):
