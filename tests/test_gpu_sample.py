@@ -112,6 +112,8 @@ def test_sample_ties_at_the_top_p_cut(gpu):
     lg[0, 3, 17] = 2.0                              # one finite logit
     lg[0, 4, :] = float("-inf")                     # none: token 0
     lg[0, 5, 100:200] = float("nan")                # NaN counts as -inf
+    snan = torch.tensor([0x7F81, -0x7F], dtype=torch.int16).view(torch.bfloat16)  # signalling NaNs, both signs
+    lg[0, 6, 10], lg[0, 6, 4000] = snan[0], snan[1]
     draft = torch.randint(0, V, (1, M), generator=g)
     parent_ref = torch.tensor([[-1, 0, 1, 2, 3, 4, 5]])
     pos = torch.arange(M)
