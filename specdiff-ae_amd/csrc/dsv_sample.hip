@@ -22,15 +22,19 @@
 //
 // Kernels:
 //   sample_select_kernel  one workgroup per row, only with top-p or top-k.
-//       The row maximum m; counts of d = m - y in a ladder of buckets (read
-//       off d's bits); the narrowest head {d <= theta} (at most kCap
-//       entries) that surely carries the top-p mass, or holds k entries, is
-//       gathered into LDS and sorted.  top-k is the head's k-th key; top-p
-//       takes the head's exact masses and bounds the rest of L by an fp32
-//       sum: the cut is exact when it lands on the same entry for every L in
-//       those bounds, inside the head.  The draw over the kept head entries is
-//       the row's result.  Other rows (flat rows, a large k, an undecided
-//       cut) are left to the radix kernel (status 2, with m).
+//       Pass 1: the row maximum m (packed integer extremes of the logits'
+//       bits).  Pass 2: exact y, the fp32 sum of 2^a (a = (y - m) log2 e) over
+//       the row, and per wave a region of the entries with a >= -g (g lowered
+//       and the region compacted when it would overflow).  The narrowest head
+//       {a > -theta} within the regions that carries the top-p mass (or holds
+//       k) is taken from them and sorted; rows whose regions do not hold it
+//       count a histogram of a and gather a head in further passes.  top-k is
+//       the head's k-th key; top-p takes the head's exact masses and bounds L
+//       from the fp32 sum: the cut is exact when it lands on the same entry
+//       for every L in those bounds, inside the head.  The draw over the kept
+//       head entries is the row's result.  Other rows (flat rows, a large k,
+//       an undecided cut, NaN or +inf logits) are left to the radix kernel
+//       (status 2, with m).
 //   sample_radix_kernel   one workgroup per row left open: 8-bit radix
 //       selection over the order keys of y (count-weighted for top-k,
 //       mass-weighted for top-p); the kept set (keys at or above both bounds)
@@ -327,35 +331,53 @@ __device__ __forceinline__ void finish_y(float (&y)[N], const Warp& T) {
 // this one's, so that a thread keeps up to four vector loads in flight.
 // Every lane of a wave runs the same iterations, so f may use wave ballots
 // and shuffles.  WARP = false hands f the logits themselves (NaN as -inf),
-// RAW = true the logits as loaded.
+// RAW = true the logits as loaded.  A wave's iterations whose vectors are all
+// whole (aligned rows) take unconditional loads; the rest read entry by entry
+// where needed.
 template <typename LT, int NT, bool WARP = true, bool RAW = false, typename F>
 __device__ __forceinline__ void row_sweep(const LT* x, int64_t lo, int64_t hi, const Warp& T, F&& f) {
   constexpr int N = 16 / sizeof(LT);
   constexpr int64_t kStep = (int64_t)2 * NT * N;
+  constexpr int64_t kSpan = (int64_t)(NT + 64) * N;  // a wave's two vectors lie in [b0, b0 + kSpan)
   const bool aligned = (reinterpret_cast<uintptr_t>(x) & 15) == 0;
   const int lane = threadIdx.x & 63;
   int64_t b0 = lo + (int64_t)(threadIdx.x & ~63) * N;  // uniform over the wave
-  if (b0 >= hi) return;
-  u32x4 ra = fetch_vec<LT>(x, b0 + (int64_t)lane * N, hi, aligned);
-  u32x4 rb = fetch_vec<LT>(x, b0 + (int64_t)lane * N + (int64_t)NT * N, hi, aligned);
+  auto run = [&](int64_t v0, const u32x4& r) {
+    float y[N];
+    unpack_vec<LT>(x, v0, v0 + N, true, r, y);
+    if constexpr (!RAW) finish_y<LT, WARP>(y, T);
+    f(v0, y);
+  };
+  if (aligned && b0 + kSpan <= hi) {
+    const LT* p = x + b0 + (int64_t)lane * N;
+    u32x4 ra = *reinterpret_cast<const u32x4*>(p), rb = *reinterpret_cast<const u32x4*>(p + NT * N);
+    for (;;) {
+      const bool more = b0 + kStep + kSpan <= hi;  // uniform over the wave
+      u32x4 na, nb;
+      if (more) {
+        na = *reinterpret_cast<const u32x4*>(p + kStep);
+        nb = *reinterpret_cast<const u32x4*>(p + kStep + NT * N);
+      }
+      run(b0 + (int64_t)lane * N, ra);
+      run(b0 + (int64_t)lane * N + (int64_t)NT * N, rb);
+      b0 += kStep;
+      p += kStep;
+      if (!more) break;
+      ra = na;
+      rb = nb;
+    }
+  }
   for (; b0 < hi; b0 += kStep) {
     const int64_t v0 = b0 + (int64_t)lane * N, v1 = v0 + (int64_t)NT * N;
-    u32x4 na = u32x4{0, 0, 0, 0}, nb = u32x4{0, 0, 0, 0};
-    if (b0 + kStep < hi) {
-      na = fetch_vec<LT>(x, v0 + kStep, hi, aligned);
-      nb = fetch_vec<LT>(x, v1 + kStep, hi, aligned);
-    }
     float ya[N], yb[N];
-    unpack_vec<LT>(x, v0, hi, aligned, ra, ya);
-    unpack_vec<LT>(x, v1, hi, aligned, rb, yb);
+    unpack_vec<LT>(x, v0, hi, aligned, fetch_vec<LT>(x, v0, hi, aligned), ya);
+    unpack_vec<LT>(x, v1, hi, aligned, fetch_vec<LT>(x, v1, hi, aligned), yb);
     if constexpr (!RAW) {
       finish_y<LT, WARP>(ya, T);
       finish_y<LT, WARP>(yb, T);
     }
     f(v0, ya);
     f(v1, yb);
-    ra = na;
-    rb = nb;
   }
 }
 
@@ -461,44 +483,258 @@ __device__ __forceinline__ int scan_desc(const uint64_t* w, uint64_t target, uin
   return __shfl(found, first);
 }
 
+// ---- select kernel helpers ----------------------------------------------------
+
+// Bits of the logits dtype read as signed integers: non-negative values order
+// as their integers and negative ones in reverse, so the integer maximum is the
+// largest non-negative value and the integer minimum the negative value
+// closest to zero.  kInf / kNegInf: the integers of +inf and -inf.
+template <typename LT>
+struct IntOrder;
+template <>
+struct IntOrder<uint16_t> {
+  static constexpr int kInf = 0x7F80, kNegInf = -0x80;
+};
+template <>
+struct IntOrder<_Float16> {
+  static constexpr int kInf = 0x7C00, kNegInf = -0x400;
+};
+template <>
+struct IntOrder<float> {
+  static constexpr int kInf = 0x7F800000, kNegInf = -0x800000;
+};
+
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+
+// The logit whose bits read as the signed integer b.
+template <typename LT>
+__device__ __forceinline__ float int_to_f(int b) {
+  if constexpr (sizeof(LT) == 4)
+    return __int_as_float(b);
+  else
+    return raw_to_f<LT>(__builtin_bit_cast(LT, (uint16_t)b));
+}
+
+// This thread's maximum of the row's logits (NaN counts as -inf) over the
+// vectors row_sweep would hand it: two integer extremes per packed word, then
+// the float they stand for.  A thread that met a positive NaN (it would pass
+// for the maximum) redoes its vectors entry by entry.
 template <typename LT, int NT>
-__global__ void __launch_bounds__(NT) sample_select_kernel(const AcceptArgs a) {
+__device__ __forceinline__ float thread_max(const LT* x, int64_t hi) {
+  constexpr int N = 16 / sizeof(LT);
+  constexpr int64_t kStep = (int64_t)NT * N;
+  using IO = IntOrder<LT>;
+  const bool aligned = (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+  const int64_t first = (int64_t)threadIdx.x * N;
+  auto word = [&](int64_t v0, int w) -> uint32_t {  // entries past hi read as -inf
+    if constexpr (sizeof(LT) == 4) {
+      return v0 + w < hi ? __builtin_bit_cast(uint32_t, x[v0 + w]) : (uint32_t)IO::kNegInf;
+    } else {
+      const uint32_t ninf = (uint32_t)IO::kNegInf & 0xFFFFu;
+      const uint32_t lo = v0 + 2 * w < hi ? (uint32_t)__builtin_bit_cast(uint16_t, x[v0 + 2 * w]) : ninf;
+      const uint32_t hi16 = v0 + 2 * w + 1 < hi ? (uint32_t)__builtin_bit_cast(uint16_t, x[v0 + 2 * w + 1]) : ninf;
+      return lo | (hi16 << 16);
+    }
+  };
+  int hmax, hmin;
+  if constexpr (sizeof(LT) == 4) {
+    int pmax = INT32_MIN, nmin = INT32_MAX;
+    auto take = [&](const u32x4& r) {
+      pmax = max(max(pmax, (int)r[0]), max((int)r[1], max((int)r[2], (int)r[3])));
+      nmin = min(min(nmin, (int)r[0]), min((int)r[1], min((int)r[2], (int)r[3])));
+    };
+    int64_t v0 = first;
+    for (; aligned && v0 + 3 * kStep + N <= hi; v0 += 4 * kStep) {
+      u32x4 r[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) r[u] = *reinterpret_cast<const u32x4*>(x + v0 + u * kStep);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) take(r[u]);
+    }
+    for (; v0 < hi; v0 += kStep) {
+      u32x4 r;
+      if (aligned && v0 + N <= hi)
+        r = *reinterpret_cast<const u32x4*>(x + v0);
+      else
+        r = u32x4{word(v0, 0), word(v0, 1), word(v0, 2), word(v0, 3)};
+      take(r);
+    }
+    hmax = pmax;
+    hmin = nmin;
+  } else {
+    s16x2 pmax = {(short)-32768, (short)-32768}, nmin = {(short)32767, (short)32767};
+    auto take = [&](const u32x4& r) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t rw = r[w];  // (a bit cast of the element itself reads element 0)
+        const s16x2 s = __builtin_bit_cast(s16x2, rw);
+        pmax = __builtin_elementwise_max(pmax, s);
+        nmin = __builtin_elementwise_min(nmin, s);
+      }
+    };
+    int64_t v0 = first;
+    for (; aligned && v0 + 3 * kStep + N <= hi; v0 += 4 * kStep) {
+      u32x4 r[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) r[u] = *reinterpret_cast<const u32x4*>(x + v0 + u * kStep);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) take(r[u]);
+    }
+    for (; v0 < hi; v0 += kStep) {
+      u32x4 r;
+      if (aligned && v0 + N <= hi)
+        r = *reinterpret_cast<const u32x4*>(x + v0);
+      else
+        r = u32x4{word(v0, 0), word(v0, 1), word(v0, 2), word(v0, 3)};
+      take(r);
+    }
+    hmax = max((int)pmax.x, (int)pmax.y);
+    hmin = min((int)nmin.x, (int)nmin.y);
+  }
+  if (hmax > IO::kInf) {  // a positive NaN: entry by entry, NaN as -inf
+    float m = kNegInfF;
+    for (int64_t v0 = first; v0 < hi; v0 += kStep)
+      for (int e = 0; e < N && v0 + e < hi; ++e) m = fmaxf(m, clean_y(raw_to_f<LT>(x[v0 + e])));
+    return m;
+  }
+  if (hmax >= 0) return int_to_f<LT>(hmax);
+  if (hmin <= IO::kNegInf) return int_to_f<LT>(hmin);
+  return kNegInfF;  // no entries, or only negative NaNs
+}
+
+// warp_vec without clean_y (NaN stays NaN, -0 stays -0), for 16-bit logits:
+// y = x / T rounded to the dtype, from q = x * fl(1/T).  q lies within 3 fp32
+// ulp of the correctly rounded quotient (for bf16 also among the subnormals,
+// whose spacing is that of the smallest binade and whose bf16 rounding reads
+// the same low 16 bits), so both round to the same 16-bit value unless q is
+// within 8 ulp of a rounding midpoint; the division decides there and, for
+// f16, outside its normal range.
+template <typename LT, int N>
+__device__ __forceinline__ void warp_vec_raw(float (&y)[N], const Warp& w) {
+  if constexpr (sizeof(LT) == 2) {
+    constexpr bool kF16 = __is_same(LT, _Float16);
+    constexpr int LOW = kF16 ? 13 : 16;
+    constexpr uint32_t MID = 1u << (LOW - 1);
+    float q[N];
+    bool unsafe[N], any = false;
+#pragma unroll
+    for (int e = 0; e < N; ++e) {
+      q[e] = y[e] * w.rT;
+      const uint32_t low = __float_as_uint(q[e]) & ((1u << LOW) - 1u);
+      bool u = low - (MID - 8u) <= 16u;
+      if constexpr (kF16) {
+        const float aq = fabsf(q[e]);
+        u |= !(aq >= 0x1p-14f && aq <= 32768.f);
+      }
+      unsafe[e] = u;
+      any |= u;
+    }
+    if (__ballot(any) != 0ull) {
+#pragma unroll
+      for (int e = 0; e < N; ++e)
+        if (unsafe[e]) q[e] = y[e] / w.T;
+    }
+#pragma unroll
+    for (int e = 0; e < N; ++e) y[e] = round_lt<LT>(q[e]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < N; ++e) y[e] = y[e] / w.T;
+  }
+}
+
+// The smallest logit x (in the dtype's order, NaN excluded) whose warped y is
+// at least thr; thr is finite, so +inf qualifies.  The warper is monotone,
+// so {x : y(x) >= thr} = {x >= result}.  Wave-parallel search over the order
+// keys: each round the 64 lanes test 64 evenly spaced keys.  Every lane of
+// the wave calls it and gets the result.
+template <typename LT>
+__device__ __forceinline__ float x_threshold(float thr, const Warp& w) {
+  constexpr bool k16 = sizeof(LT) == 2;
+  const uint32_t sign = k16 ? 0x8000u : 0x80000000u, all = k16 ? 0xFFFFu : 0xFFFFFFFFu;
+  const uint32_t inf = (uint32_t)IntOrder<LT>::kInf, ninf = ((uint32_t)IntOrder<LT>::kNegInf) & all;
+  auto key_of = [&](uint32_t b) { return (b & sign) ? (b ^ all) : (b ^ sign); };
+  auto bits_of = [&](uint32_t k) { return (k & sign) ? (k ^ sign) : (k ^ all); };
+  auto passes = [&](uint32_t k) {
+    const uint32_t b = bits_of(k);
+    return warp_yf<LT>(int_to_f<LT>((int)b), w) >= thr;
+  };
+  const int lane = threadIdx.x & 63;
+  uint64_t lo = key_of(ninf), hi = key_of(inf);  // the answer lies in [lo, hi]
+  while (lo < hi) {
+    const uint64_t step = (hi - lo + 64) / 64;
+    const uint64_t p = min(lo + (uint64_t)(lane + 1) * step - 1, hi);
+    const uint64_t bal = __ballot(passes((uint32_t)p));
+    const int l = __builtin_ctzll(bal);  // the last lane tests hi, which passes
+    const uint64_t nhi = min(lo + (uint64_t)(l + 1) * step - 1, hi);
+    lo = l == 0 ? lo : lo + (uint64_t)l * step;
+    hi = nhi;
+  }
+  return int_to_f<LT>((int)bits_of((uint32_t)lo));
+}
+
+// Histogram bins of a = (y - m) log2 e, read off |a|'s bits (exponent and first
+// mantissa bit): bin 0 holds |a| < kTheta[0], bin j (1..15) kTheta[j-1] <= |a|
+// < kTheta[j], bin 16 the rest (and NaN).
+constexpr int kBins = kNTheta + 1;
+// The statistics pass also keeps, per wave, the entries with a >= -g in a
+// region of kCap / waves entries: g starts at kPreG0 and drops by 2 (the
+// region compacted) whenever the region would overflow, down to kPreGMin.
+// a is the same fp32 expression wherever it is evaluated, and monotone in y,
+// so {a >= -theta} is a head of the order, held by the regions when theta <=
+// the smallest g of the waves.
+constexpr float kPreG0 = 16.f, kPreGMin = 2.f;
+constexpr int kPre = 2048;  // entries of the regions of a block
+
+// Four waves per SIMD (at most 128 VGPRs): two 512-thread rows share a CU.
+template <typename LT, int NT>
+__global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) sample_select_kernel(const AcceptArgs a) {
   static_assert(kCap % NT == 0, "candidates split evenly over the threads");
+  constexpr int kWaves = NT / 64;
+  constexpr int kHistWords = kWaves * kBins * 64;
+  constexpr int kPreCap = kPre / kWaves;  // entries of a wave's region of pre
+  static_assert(kHistWords >= 2 * kCap && kCap >= 2 * NT, "the candidates (and a sorted copy of up to NT) fit where the histograms were");
   const int64_t row = blockIdx.x;
   const int t = (int)(row / a.M), i = (int)(row % a.M);
   const LT* x = reinterpret_cast<const LT*>(a.logits) + (int64_t)t * a.l_st + (int64_t)i * a.l_sm;
   const int V = (int)a.V;
   const int tid = threadIdx.x;
-  constexpr int ND = key_digits<LT>();
+  const int lane = tid & 63, wv = tid >> 6;
   const Warp wp = make_warp(a.temperature);
+  constexpr int NV = 16 / sizeof(LT);
 
-  __shared__ float red_f[NT / 64];
+  // hist: the per-lane histograms of the statistics pass, then the head's
+  // candidates ((key << 32) | index).  pre: the waves' regions of entries near
+  // the maximum, (index << 32) | bits of y.
+  __shared__ __align__(16) uint32_t hist[kHistWords];
+  __shared__ __align__(16) uint64_t pre[kPre];
+  uint64_t* cand = reinterpret_cast<uint64_t*>(hist);
+  __shared__ float red_f[kWaves];
+  __shared__ uint32_t pre_n[kWaves];
+  __shared__ float pre_g[kWaves];
+  __shared__ float wbin_q[kWaves][kBins];
+  __shared__ uint32_t wbin_c[kWaves][kBins];
+  __shared__ uint32_t cnt_th[kNTheta];
+  __shared__ uint32_t ncand, nk_lo, nk_hi;
+  __shared__ int jsel[3];
+  __shared__ float xthr_s;
+  __shared__ uint64_t red_q[kWaves];
+  __shared__ double red_d[kWaves];
+  __shared__ int red_i[kWaves];
 
   // Row maximum of y: the warper is monotone, so it is the warped maximum
   // logit (xm).
-  float m = kNegInfF;
-  constexpr int NV = 16 / sizeof(LT);
-  row_sweep<LT, NT, false>(x, 0, V, wp, [&](int64_t, const float(&y)[NV]) {
-#pragma unroll
-    for (int e = 0; e < NV; ++e) m = fmaxf(m, y[e]);
-  });
+  float m = thread_max<LT, NT>(x, V);
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-  if ((tid & 63) == 0) red_f[tid >> 6] = m;
+  if (lane == 0) red_f[wv] = m;
   __syncthreads();
-  if (tid == 0) {
-    float mm = red_f[0];
-    for (int w = 1; w < NT / 64; ++w) mm = fmaxf(mm, red_f[w]);
-    red_f[0] = mm;
-  }
-  __syncthreads();
-  const float xm = red_f[0];
+  float xm = red_f[0];
+  for (int w = 1; w < kWaves; ++w) xm = fmaxf(xm, red_f[w]);
   m = xm > kNegInfF ? warp_y<LT>(f_to_raw<LT>(xm), wp) : kNegInfF;
 
   int S = 63;
   for (int vv = V; vv > 0; vv >>= 1) --S;  // 63 - bitlen(V)
 
-  const int lane = tid & 63, wv = tid >> 6;
   const int64_t kk = (a.top_k > 0 && a.top_k < V) ? a.top_k : 0;
   const bool use_p = a.top_p_q != 0;
   // The row's draw, written by thread 0 as range 0's result (the other
@@ -519,195 +755,327 @@ __global__ void __launch_bounds__(NT) sample_select_kernel(const AcceptArgs a) {
     if (tid == 0) a.sel[row] = make_uint4(0u, 0u, 0u, 0u);
     return;
   }
+  if (!(m < -kNegInfF)) {  // +inf maximum: the radix kernel's exact masses
+    if (tid == 0) a.sel[row] = make_uint4(__float_as_uint(m), 0u, 0u, 2u);
+    return;
+  }
 
-  // ---- fast path --------------------------------------------------------------
-  __shared__ uint64_t cand[kCap];  // (key << 32) | index, sorted descending
-  __shared__ uint32_t cnt_th[kNTheta];
-  __shared__ uint32_t ncand, nk_lo, nk_hi;
-  __shared__ int jsel[2];
-  __shared__ uint32_t n_eq;
-  __shared__ float red_l[NT / 64];
-  __shared__ uint64_t red_q[NT / 64];
-  __shared__ double red_d[NT / 64];
-  __shared__ int red_i[NT / 64];
-
-  if (tid < kNTheta) cnt_th[tid] = 0;
+  // ---- statistics: exact y, the fp32 sum of 2^a, the entries near m ---------
+  for (int q = tid; q < kWaves * kBins; q += NT) {
+    wbin_c[q / kBins][q % kBins] = 0;
+    wbin_q[q / kBins][q % kBins] = 0.f;
+  }
   if (tid == 0) {
     ncand = 0;
     nk_lo = 0;
     nk_hi = 0;
-    n_eq = 0;
   }
   __syncthreads();
-  // Counts of d = (xm - x) / T (fp32, equal to m - y when T == 1; close to
-  // it otherwise, the gather below checks the count) per bucket b: d <= theta_0 (b = 0),
-  // theta_(b-1) < d <= theta_b (b = 1..15), read off d's bits (exponent and
-  // first mantissa bit); a lane keeps them as 8-bit fields of two words (at
-  // most 16 * 8 entries between flushes).
-  {
-    uint32_t cth[kNTheta];
+  const float mc = m * 0x1.715476p+0f;
+  // a of a logit's warped value: the one fp32 expression used for every decision on a.
+  auto a_of = [&](float y) { return fmaf(y, 0x1.715476p+0f, -mc); };
+  uint64_t* pw = pre + wv * kPreCap;
+  // Per-wave bins of the appended entries (count of bin b at wbin_c[wv][b],
+  // fp32 mass at wbin_q[wv][b]); bins past the final bound also count entries
+  // the compaction dropped, and are not used.
+  uint32_t pcnt = 0;   // entries in this wave's region (the same in every lane)
+  float gw = kPreG0;   // this wave's bound (the same in every lane); below kPreGMin: given up
+  float lsum = 0.f;    // top-p: sum of 2^a over the row (fp32)
+  // Keeps the region's entries with a >= -gw, in order (the wave's lanes read
+  // a chunk before they write below it).
+  auto compact = [&]() {
+    uint32_t nk = 0;
+    for (uint32_t s0 = 0; s0 < pcnt; s0 += 64) {
+      const uint32_t q = s0 + (uint32_t)lane;
+      const uint64_t cv = q < pcnt ? pw[q] : 0ull;
+      const bool keep = q < pcnt && a_of(__uint_as_float((uint32_t)cv)) >= -gw;
+      const uint64_t bal = __ballot(keep);
+      if (keep) pw[nk + (uint32_t)__popcll(bal & ((1ull << lane) - 1ull))] = cv;
+      nk += (uint32_t)__popcll(bal);
+    }
+    pcnt = nk;
+  };
+  row_sweep<LT, NT, false, true>(x, 0, V, wp, [&](int64_t v0, const float(&xv)[NV]) {
+    float y[NV], ar[NV];
 #pragma unroll
-    for (int j = 0; j < kNTheta; ++j) cth[j] = 0;
-    uint64_t pk0 = 0, pk1 = 0;
-    int calls = 0;
-    float lsum = 0.f;  // top-p: sum of e^-d (fp32), for the choice of the head
-    uint32_t eq = 0;   // entries at the maximum (d == 0, mass 1 each)
-    auto flush = [&]() {
+    for (int e = 0; e < NV; ++e) y[e] = xv[e];
+    if (wp.T != 1.f) warp_vec_raw<LT, NV>(y, wp);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        cth[j] += (uint32_t)(pk0 >> (8 * j)) & 0xFFu;
-        cth[j + 8] += (uint32_t)(pk1 >> (8 * j)) & 0xFFu;
-      }
-      pk0 = 0;
-      pk1 = 0;
-    };
-    row_sweep<LT, NT, false>(x, 0, V, wp, [&](int64_t, const float(&y)[NV]) {
+    for (int e = 0; e < NV; ++e) {
+      ar[e] = a_of(y[e]);
+      if (use_p) lsum += __builtin_amdgcn_exp2f(ar[e]);  // NaN y: the sum is NaN
+    }
+    // This vector's entries near the maximum, appended to the wave's region
+    // (the bound lowered first while they would overflow it).
+    uint64_t bal[NV];
+    uint32_t tot = 0;
 #pragma unroll
-      for (int e = 0; e < NV; ++e) {
-        const float d = (xm - y[e]) * wp.rT;
-        const int b = min(max((((int)__float_as_uint(d) - 1) >> 22) - 249, 0), kNTheta);
-        const uint64_t inc = 1ull << (8 * (b & 7));
-        pk0 += b < 8 ? inc : 0ull;
-        pk1 += (b >= 8 && b < kNTheta) ? inc : 0ull;
-        if (use_p) {
-          lsum += __builtin_amdgcn_exp2f(d * -1.44269504088896341f);
-          eq += d == 0.f ? 1u : 0u;
+    for (int e = 0; e < NV; ++e) {
+      bal[e] = __ballot(ar[e] >= -gw);
+      tot += (uint32_t)__popcll(bal[e]);
+    }
+    if (tot != 0u && gw >= kPreGMin) {
+      while (pcnt + tot > (uint32_t)kPreCap && gw >= kPreGMin) {
+        gw -= 2.f;
+        compact();
+        tot = 0;
+#pragma unroll
+        for (int e = 0; e < NV; ++e) {
+          bal[e] = __ballot(ar[e] >= -gw);
+          tot += (uint32_t)__popcll(bal[e]);
         }
       }
-      if (++calls == 16) {
-        flush();
-        calls = 0;
+      if (gw >= kPreGMin) {
+#pragma unroll
+        for (int e = 0; e < NV; ++e) {
+          if (bal[e] != 0ull) {
+            if ((bal[e] >> lane) & 1ull) {
+              pw[pcnt + (uint32_t)__popcll(bal[e] & ((1ull << lane) - 1ull))] =
+                  ((uint64_t)(uint32_t)(v0 + e) << 32) | __float_as_uint(y[e]);
+              const uint32_t b = min(max((__float_as_uint(ar[e]) >> 22) & 0x1FFu, 249u), 249u + kNTheta) - 249u;
+              atomicAdd(&wbin_c[wv][b], 1u);
+              atomicAdd(&wbin_q[wv][b], __builtin_amdgcn_exp2f(ar[e]));
+            }
+            pcnt += (uint32_t)__popcll(bal[e]);
+          }
+        }
+      }
+    }
+  });
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) lsum += __shfl_xor(lsum, o);
+  if (lane == 0) {
+    red_f[wv] = lsum;
+    pre_n[wv] = pcnt;
+    pre_g[wv] = gw;
+  }
+  __syncthreads();
+  float L = 0.f, gcov = kPreG0;  // the regions hold every entry with a >= -gcov
+  for (int w = 0; w < kWaves; ++w) {
+    L += red_f[w];
+    gcov = fminf(gcov, pre_g[w]);
+  }
+  if (use_p && !(L == L)) {  // NaN logits (NaN counts as -inf): the radix kernel
+    if (tid == 0) a.sel[row] = make_uint4(__float_as_uint(m), 0u, 0u, 2u);
+    return;
+  }
+  const float need = (float)a.top_p_q * 0x1p-32f * L * (1.f + 0x1p-8f);
+  // Counts and fp32 masses of the regions' entries per bin of a (bin 0: |a| <
+  // kTheta[0], bin j: kTheta[j-1] <= |a| < kTheta[j], read off |a|'s exponent
+  // and first mantissa bit); with gcov >= kTheta[j], bins 0..j of the regions
+  // are the whole head {a > -kTheta[j]}.
+  if (wv == 0) {
+    // The narrowest head within gcov whose fp32 mass reaches top_p of the
+    // total (top-k alone: holding k), marked kNTheta + j (taken from the
+    // regions): lane j sums bin j over the waves, then inclusive prefix sums.
+    float hq = 0.f;
+    uint32_t hc = 0;
+    if (lane < kNTheta) {
+      for (int w = 0; w < kWaves; ++w) {
+        hq += wbin_q[w][lane];
+        hc += wbin_c[w][lane];
+      }
+    }
+#pragma unroll
+    for (int o = 1; o < kNTheta; o <<= 1) {
+      const float q2 = __shfl_up(hq, o);
+      const uint32_t c2 = __shfl_up(hc, o);
+      if (lane >= o) {
+        hq += q2;
+        hc += c2;
+      }
+    }
+    const bool reach = lane < kNTheta && gcov >= kPreGMin && kTheta[lane < kNTheta ? lane : 0] <= gcov &&
+                       (use_p ? hq >= need : hc >= (uint64_t)kk);
+    const uint64_t bal = __ballot(reach);
+    if (lane == 0) {
+      jsel[0] = bal != 0ull ? kNTheta + __builtin_ctzll(bal) : -1;
+      jsel[1] = -2;  // the histogram's heads: not counted yet
+    }
+  }
+  __syncthreads();
+
+  // Histogram of a over the row, for the rows whose regions do not hold the
+  // cut: per-lane counts in LDS (hist), then jsel[1..2]: top-k alone, the
+  // narrowest head holding k; top-p, first the narrowest head whose mass
+  // surely reaches top_p of the total (an entry of bin j has mass above
+  // 2^-kTheta[j]), then the widest head that fits.
+  auto histogram_heads = [&]() {
+    for (int q = tid; q < kHistWords; q += NT) hist[q] = 0;
+    if (tid < kNTheta) cnt_th[tid] = 0;
+    __syncthreads();
+    uint32_t* hb = hist + wv * kBins * 64 + lane - 249 * 64;  // bin b9 - 249 of this lane at hb[b9 * 64]
+    row_sweep<LT, NT, false, true>(x, 0, V, wp, [&](int64_t, const float(&xv)[NV]) {
+      float y[NV];
+#pragma unroll
+      for (int e = 0; e < NV; ++e) y[e] = xv[e];
+      if (wp.T != 1.f) warp_vec_raw<LT, NV>(y, wp);
+#pragma unroll
+      for (int e = 0; e < NV; ++e) {
+        const uint32_t b9 = min(max((__float_as_uint(a_of(y[e])) >> 22) & 0x1FFu, 249u), 249u + kNTheta);
+        atomicAdd(hb + b9 * 64, 1u);
       }
     });
-    flush();
-    // Cumulative: cth[j] = #{d <= theta_j}; then the block's sums.
+    __syncthreads();
+    uint32_t c = 0, cth[kNTheta];
 #pragma unroll
-    for (int j = 1; j < kNTheta; ++j) cth[j] += cth[j - 1];
+    for (int j = 0; j < kNTheta; ++j) {
+      c += hb[(249 + j) * 64];
+      cth[j] = c;
+    }
 #pragma unroll
     for (int j = 0; j < kNTheta; ++j) {
 #pragma unroll
       for (int o = 32; o > 0; o >>= 1) cth[j] += __shfl_xor(cth[j], o);
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      lsum += __shfl_xor(lsum, o);
-      eq += __shfl_xor(eq, o);
-    }
     if (lane == 0) {
 #pragma unroll
       for (int j = 0; j < kNTheta; ++j) atomicAdd(&cnt_th[j], cth[j]);
-      atomicAdd(&n_eq, eq);
-      red_l[wv] = lsum;
     }
-  }
-  __syncthreads();
-  if (tid == 0) {
-    // top-k alone: the narrowest head holding k.  top-p: first the narrowest
-    // head whose mass surely reaches top_p of the estimated total (entries at
-    // the maximum count 1, the others e^-theta of their bucket's bound), then
-    // the widest head that fits.
-    int j0 = -1, j1 = -1;
-    if (use_p) {
-      float L = 0.f;
-      for (int w = 0; w < NT / 64; ++w) L += red_l[w];
-      const float need = (float)a.top_p_q * 0x1p-32f * L * (1.f + 0x1p-8f);
-      float head = (float)n_eq + (float)(cnt_th[0] - n_eq) * __expf(-kTheta[0]);
-      for (int j = 0; j < kNTheta && cnt_th[j] <= (uint32_t)kCap; ++j) {
-        if (j > 0) head += (float)(cnt_th[j] - cnt_th[j - 1]) * __expf(-kTheta[j]);
-        if (j0 < 0 && head >= need) j0 = j;
-        j1 = j;
+    __syncthreads();
+    if (tid == 0) {
+      int j0 = -1, j1 = -1;
+      if (use_p) {
+        float head = 0.f;
+        for (int j = 0; j < kNTheta && cnt_th[j] <= (uint32_t)kCap; ++j) {
+          head += (float)(cnt_th[j] - (j > 0 ? cnt_th[j - 1] : 0u)) * exp2f(-kTheta[j]);
+          if (j0 < 0 && head >= need) j0 = j;
+          j1 = j;
+        }
+        if (j0 < 0 || j0 == j1) {
+          j0 = j1;
+          j1 = -1;
+        }
+      } else {
+        for (int j = 0; j < kNTheta && j0 < 0; ++j)
+          if (cnt_th[j] >= (uint64_t)kk && cnt_th[j] <= (uint32_t)kCap) j0 = j;
       }
-      if (j0 < 0 || j0 == j1) {
-        j0 = j1;
-        j1 = -1;
-      }
-    } else {
-      for (int j = 0; j < kNTheta && j0 < 0; ++j)
-        if (cnt_th[j] >= (uint64_t)kk && cnt_th[j] <= (uint32_t)kCap) j0 = j;
+      jsel[1] = j0;
+      jsel[2] = j1;
+      ncand = 0;
+      nk_lo = 0;
+      nk_hi = 0;
     }
-    jsel[0] = j0;
-    jsel[1] = j1;
-  }
-  __syncthreads();
-  for (int att = 0; att < 2 && jsel[att] >= 0; ++att) {
-    if (att > 0) {
-      if (tid == 0) {
-        ncand = 0;
-        nk_lo = 0;
-        nk_hi = 0;
-      }
-      __syncthreads();
+    __syncthreads();
+  };
+
+  // Attempt 0: the regions' head; attempts 1, 2: the histogram's heads.
+  for (int att = 0; att < 3; ++att) {
+    if (att == 1 && jsel[1] == -2) histogram_heads();
+    const int js = jsel[att];
+    if (js < 0) {
+      if (att == 0) continue;
+      break;
     }
-    const float ts = kTheta[jsel[att]];
-    // Gather the candidates; sum the fp32 masses of the others.
-    float tail = 0.f;
-    row_sweep<LT, NT>(x, 0, V, wp, [&](int64_t v0, const float(&y)[NV]) {
-      bool any = false;
-#pragma unroll
-      for (int e = 0; e < NV; ++e) {
-        const bool c = m - y[e] <= ts;  // a head of the order (monotone in y)
-        any |= c;
-        if (use_p && !c) tail += __builtin_amdgcn_exp2f((y[e] - m) * 1.44269504088896341f);
-      }
-      if (__ballot(any) == 0ull) return;
-#pragma unroll
-      for (int e = 0; e < NV; ++e) {
-        const bool c = m - y[e] <= ts;
+    if (att == 2 && tid == 0) {
+      ncand = 0;
+      nk_lo = 0;
+      nk_hi = 0;
+    }
+    if (att == 2) __syncthreads();
+    if (js >= kNTheta) {
+      // From the waves' regions: the head {a > -kTheta[j]} (bins 0..j).
+      const float ath = -kTheta[js - kNTheta];
+      for (int q0 = 0; q0 < kPre; q0 += NT) {
+        const int q = q0 + tid;
+        const uint64_t pv = pre[q];
+        const float yq = __uint_as_float((uint32_t)pv);
+        const bool c = (uint32_t)(q % kPreCap) < pre_n[q / kPreCap] && a_of(yq) > ath;
+        const uint64_t cv = ((uint64_t)ykey(yq == 0.f ? 0.f : yq) << 32) | (pv >> 32);
         const uint64_t bal = __ballot(c);
         if (bal != 0ull) {
           uint32_t base = 0;
           if (lane == 0) base = atomicAdd(&ncand, (uint32_t)__popcll(bal));
           base = __shfl(base, 0);
-          if (c) {
-            const uint32_t slot = base + (uint32_t)__popcll(bal & ((1ull << lane) - 1ull));
-            if (slot < (uint32_t)kCap) cand[slot] = ((uint64_t)ykey(y[e]) << 32) | (uint32_t)(v0 + e);
-          }
+          if (c) cand[base + (uint32_t)__popcll(bal & ((1ull << lane) - 1ull))] = cv;
         }
       }
-    });
+    } else {
+      // A pass over the row for the head {y >= thr}: by the warper's monotony,
+      // {x >= x_thr} on the logits.
+      const float thr = m - kTheta[js] * 0x1.62e430p-1f;
+      if (wv == 0) {
+        const float xt = x_threshold<LT>(thr, wp);
+        if (lane == 0) xthr_s = xt;
+      }
+      __syncthreads();
+      const float xthr = xthr_s;
+      row_sweep<LT, NT, false, true>(x, 0, V, wp, [&](int64_t v0, const float(&xv)[NV]) {
+        bool any = false;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) tail += __shfl_xor(tail, o);
-    if (lane == 0) red_f[wv] = tail;
-    __syncthreads();
-    const int n = min((int)ncand, kCap);
-    // The counts (of the unwarped logits when T != 1) chose the threshold;
-    // the gathered count decides whether the head fits and holds k entries.
-    const bool fits = (int)ncand <= kCap && (use_p || (int64_t)ncand >= kk);
-    float tail_all = 0.f;
-    for (int w = 0; w < NT / 64; ++w) tail_all += red_f[w];
-    // Bitonic sort, descending, padded with zero keys to a power of two.
-    int npad = 2;
-    while (npad < n) npad <<= 1;
-    for (int q = n + tid; q < npad; q += NT) cand[q] = 0ull;
-    __syncthreads();
-    for (int k2 = 2; k2 <= npad; k2 <<= 1)
-      for (int j2 = k2 >> 1; j2 > 0; j2 >>= 1) {
-        for (int q = tid; q < npad; q += NT) {
-          const int l = q ^ j2;
-          if (l > q) {
-            const uint64_t u = cand[q], w = cand[l];
-            if (((q & k2) == 0) ? (u < w) : (u > w)) {
-              cand[q] = w;
-              cand[l] = u;
+        for (int e = 0; e < NV; ++e) any |= xv[e] >= xthr;
+        if (__ballot(any) == 0ull) return;
+#pragma unroll
+        for (int e = 0; e < NV; ++e) {
+          const bool c = xv[e] >= xthr;
+          const uint64_t bal = __ballot(c);
+          if (bal != 0ull) {
+            uint32_t base = 0;
+            if (lane == 0) base = atomicAdd(&ncand, (uint32_t)__popcll(bal));
+            base = __shfl(base, 0);
+            if (c) {
+              const uint32_t slot = base + (uint32_t)__popcll(bal & ((1ull << lane) - 1ull));
+              if (slot < (uint32_t)kCap) cand[slot] = ((uint64_t)ykey(warp_yf<LT>(xv[e], wp)) << 32) | (uint32_t)(v0 + e);
             }
           }
         }
-        __syncthreads();
+      });
+    }
+    __syncthreads();
+    const int n = min((int)ncand, kCap);
+    // The counts chose the threshold; the gathered count decides whether the
+    // head fits and holds k entries.
+    const bool fits = (int)ncand <= kCap && (use_p || (int64_t)ncand >= kk);
+    // Sorted descending: up to NT entries by rank (keys are distinct: they
+    // carry the index) into cand[NT, 2 NT); more by a bitonic sort in place,
+    // padded with zero keys to a power of two.
+    const uint64_t* keys = cand;
+    if (n <= NT) {
+      uint64_t* out = cand + NT;  // above the n <= NT candidates
+      if (tid < n) {
+        const uint64_t mine = cand[tid];
+        int rank = 0;
+#pragma unroll 8
+        for (int j = 0; j < n; ++j) rank += cand[j] > mine ? 1 : 0;
+        out[rank] = mine;
       }
+      keys = out;
+    } else {
+      int npad = 2;
+      while (npad < n) npad <<= 1;
+      for (int q = n + tid; q < npad; q += NT) cand[q] = 0ull;
+      __syncthreads();
+      for (int k2 = 2; k2 <= npad; k2 <<= 1)
+        for (int j2 = k2 >> 1; j2 > 0; j2 >>= 1) {
+          for (int q = tid; q < npad; q += NT) {
+            const int l = q ^ j2;
+            if (l > q) {
+              const uint64_t u = cand[q], w = cand[l];
+              if (((q & k2) == 0) ? (u < w) : (u > w)) {
+                cand[q] = w;
+                cand[l] = u;
+              }
+            }
+          }
+          __syncthreads();
+        }
+    }
+    __syncthreads();
     // top-k: the k-th key when the candidates hold k (else every candidate
     // passes top-k, and the cut comes from top-p inside the candidates).
-    const uint32_t tk = (kk > 0 && n >= kk) ? (uint32_t)(cand[kk - 1] >> 32) : 0u;
+    const uint32_t tk = (kk > 0 && n >= kk) ? (uint32_t)(keys[kk - 1] >> 32) : 0u;
     int nkeep = n;
     bool ok = fits;
     if (use_p && ok) {
-      // Exact masses along the order (thread tid holds entries EPT * tid ..
-      // + EPT - 1) and their exclusive prefix sums.
+      // Exact masses along the order (thread tid holds entries ept * tid ..
+      // + ept - 1) and their exclusive prefix sums.
       constexpr int EPT = kCap / NT;
+      const int ept = (n + NT - 1) / NT;
       uint64_t qv[EPT], tot = 0;
 #pragma unroll
       for (int u = 0; u < EPT; ++u) {
-        const int e = EPT * tid + u;
-        qv[u] = e < n ? fixed_mass(key_to_y((uint32_t)(cand[e] >> 32)), m, S) : 0ull;
+        const int e = ept * tid + u;
+        qv[u] = (u < ept && e < n) ? fixed_mass(key_to_y((uint32_t)(keys[e] >> 32)), m, S) : 0ull;
         tot += qv[u];
       }
       uint64_t incl = tot;
@@ -719,21 +1087,29 @@ __global__ void __launch_bounds__(NT) sample_select_kernel(const AcceptArgs a) {
       if (lane == 63) red_q[wv] = incl;
       __syncthreads();
       uint64_t wbase = 0, H = 0;
-      for (int w = 0; w < NT / 64; ++w) {
+      for (int w = 0; w < kWaves; ++w) {
         if (w < wv) wbase += red_q[w];
         H += red_q[w];
       }
-      // L = H + (masses outside the candidates), bounded from the fp32 sum.
-      const double tr = (double)tail_all * __builtin_ldexp(1.0, S);
-      const double tlo = __builtin_fmax(0.0, tr * (1.0 - 0x1p-12) - (double)V);
-      const double thi = __builtin_fmin(tr * (1.0 + 0x1p-12) + (double)V + 1.0, 0x1p62);
-      const uint64_t tq_lo = tq_of(a.top_p_q, H + (uint64_t)__builtin_floor(tlo));
-      const uint64_t tq_hi = tq_of(a.top_p_q, H + (uint64_t)__builtin_ceil(thi));
+      // L = sum of the exact masses, bounded from the fp32 sum of 2^a over the
+      // row: relative error below (summands per thread + 8 + waves) 2^-24
+      // from the sum, 2^-16 from the hardware 2^x and the rounding of a
+      // (|a| <= 64; smaller masses are within the integer slack), and 2^-22 |m|
+      // from the rounding of m log2 e; each mass's integer rounding adds V.
+      const double Lq = (double)L * __builtin_ldexp(1.0, S);
+      const double eps = ((double)((V + NT - 1) / NT) + 8.0 + kWaves) * 0x1p-24 + 0x1p-16 +
+                         0x1p-22 * __builtin_fabs((double)m);
+      const double llo = __builtin_fmax(0.0, Lq * (1.0 - eps) - (double)V);
+      const double lhi = __builtin_fmin(Lq * (1.0 + eps) + (double)V + 1.0, 0x1p62);
+      const uint64_t L_lo = max(H, (uint64_t)__builtin_floor(llo));
+      const uint64_t L_hi = max(H, (uint64_t)__builtin_ceil(lhi));
+      const uint64_t tq_lo = tq_of(a.top_p_q, L_lo);
+      const uint64_t tq_hi = tq_of(a.top_p_q, L_hi);
       uint32_t cl = 0, ch = 0;
       uint64_t above = wbase + incl - tot;
 #pragma unroll
       for (int u = 0; u < EPT; ++u) {
-        if (EPT * tid + u < n) {
+        if (u < ept && ept * tid + u < n) {
           cl += above < tq_lo;
           ch += above < tq_hi;
         }
@@ -758,7 +1134,7 @@ __global__ void __launch_bounds__(NT) sample_select_kernel(const AcceptArgs a) {
       double bz = -__builtin_huge_val();
       int bi = -1;
       for (int q = tid; q < n; q += NT) {
-        const uint64_t cv = cand[q];
+        const uint64_t cv = keys[q];
         const uint32_t key = (uint32_t)(cv >> 32);
         const int v = (int)(uint32_t)cv;
         if (q < nkeep && key >= tk) {
