@@ -61,8 +61,9 @@ constexpr int kRadixThreads = 1024;
 constexpr int kSweepThreads = 256;
 constexpr float kNegInfF = -__builtin_huge_valf();
 constexpr int kCap = 4096;   // candidates the select kernel's fast path sorts in LDS
-// Ladder of candidate thresholds m - y <= theta_j: the floats whose bits are
-// (250 + j) << 22, i.e. 2^e and 1.5 * 2^e from 1/4 to 48.
+// Head thresholds of the select kernel, in log2 units of a = (y - m) log2 e
+// (the head {a > -theta_j}): the floats whose bits are (250 + j) << 22, i.e.
+// 2^e and 1.5 * 2^e from 1/4 to 48.
 constexpr int kNTheta = 16;
 __constant__ float kTheta[kNTheta] = {0.25f, 0.375f, 0.5f, 0.75f, 1.f, 1.5f, 2.f, 3.f,
                                       4.f,   6.f,    8.f,  12.f,  16.f, 24.f, 32.f, 48.f};
