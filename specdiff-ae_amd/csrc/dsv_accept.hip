@@ -206,6 +206,12 @@ __device__ __forceinline__ float half_to_f(uint32_t h) {
   return __uint_as_float(h << 16);
 }
 __device__ __forceinline__ uint32_t key_to_bits(uint32_t k) { return (k & 0x8000u) ? (k ^ 0x8000u) : (~k & 0xFFFFu); }
+// The bits of a 16-bit value held exactly as a float.
+template <bool F16>
+__device__ __forceinline__ uint32_t f_to_half_bits(float x) {
+  if constexpr (F16) return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
+  return __float_as_uint(x) >> 16;
+}
 
 template <bool F16, bool TYPICAL>
 __global__ void __launch_bounds__(kStrThreads) accept_stream16_kernel(const AcceptArgs a) {
@@ -253,6 +259,60 @@ __global__ void __launch_bounds__(kStrThreads) accept_stream16_kernel(const Acce
   auto reduce_sub = [&](int s, u32x4 (&r)[kStrVec]) {
     if (s == nsub - 1) pad_tail(s, r);
     if (nan_i != 0x7fffffff) return;  // this thread's result is already NaN
+    if constexpr (TYPICAL) {
+      // The values as floats: their NaN-propagating maximum gives the NaN
+      // test, the key of the maximum (+0 for a zero maximum: IEEE maximum
+      // orders -0 below +0) and the softmax's reference.  The exponentials
+      // then read the words again with -inf raised to the lowest finite value.
+      float xv[kStrVec * 8];
+#pragma unroll
+      for (int v = 0; v < kStrVec; ++v)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          xv[8 * v + 2 * w] = half_to_f<F16>(r[v][w] & 0xFFFFu);
+          xv[8 * v + 2 * w + 1] = half_to_f<F16>(r[v][w] >> 16);
+        }
+      float vmax = xv[0];
+#pragma unroll
+      for (int e = 1; e < kStrVec * 8; ++e) vmax = __builtin_elementwise_maximum(vmax, xv[e]);
+      if (vmax != vmax) {  // rare: locate the first NaN
+#pragma unroll
+        for (int v = 0; v < kStrVec; ++v) {
+          const int vi = s * kSubVec + tid + kStrThreads * v;
+          for (int w = 0; w < 8 && nan_i == 0x7fffffff; ++w)
+            if (vi < nvec && ((r[v][w >> 1] >> (16 * (w & 1))) & 0x7FFFu) > kNanAbove) nan_i = 8 * vi + w;
+        }
+        return;
+      }
+      const uint32_t km = key2(f_to_half_bits<F16>(vmax)) & 0xFFFFu;
+      if (km > bk) {  // a larger maximum; its index is located at the end
+        bk = km;
+        bs = s;
+      }
+      const float mt = vmax * zs;
+      if (mt > m) {
+        const float sc = __builtin_amdgcn_exp2f(m - mt);  // m = -inf: 0
+        l *= sc;
+        sx *= sc;
+        m = mt;
+      }
+      if (m != kNegInf) {
+        float la = 0.f;
+#pragma unroll
+        for (int v = 0; v < kStrVec; ++v)
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const uint32_t cw = pk_min(r[v][w], kLowest2);  // -inf -> lowest finite (bits order = value order for < 0)
+            const float x0 = half_to_f<F16>(cw & 0xFFFFu), x1 = half_to_f<F16>(cw >> 16);
+            const float p0 = __builtin_amdgcn_exp2f(fmaf(x0, zs, -m));
+            const float p1 = __builtin_amdgcn_exp2f(fmaf(x1, zs, -m));
+            la += p0 + p1;
+            sx = fmaf(x0, p0, fmaf(x1, p1, sx));
+          }
+        l += la;
+      }
+      return;
+    }
     uint32_t amax = 0, km = 0;
 #pragma unroll
     for (int v = 0; v < kStrVec; ++v)
@@ -275,30 +335,6 @@ __global__ void __launch_bounds__(kStrThreads) accept_stream16_kernel(const Acce
     if (km > bk) {  // a larger maximum; its index is located at the end
       bk = km;
       bs = s;
-    }
-    if constexpr (TYPICAL) {
-      const float mt = half_to_f<F16>(key_to_bits(km)) * zs;
-      if (mt > m) {
-        const float sc = __builtin_amdgcn_exp2f(m - mt);  // m = -inf: 0
-        l *= sc;
-        sx *= sc;
-        m = mt;
-      }
-      if (m != kNegInf) {
-        float la = 0.f;
-#pragma unroll
-        for (int v = 0; v < kStrVec; ++v)
-#pragma unroll
-          for (int w = 0; w < 4; ++w) {
-            const uint32_t cw = pk_min(r[v][w], kLowest2);  // -inf -> lowest finite (bits order = value order for < 0)
-            const float x0 = half_to_f<F16>(cw & 0xFFFFu), x1 = half_to_f<F16>(cw >> 16);
-            const float p0 = __builtin_amdgcn_exp2f(fmaf(x0, zs, -m));
-            const float p1 = __builtin_amdgcn_exp2f(fmaf(x1, zs, -m));
-            la += p0 + p1;
-            sx = fmaf(x0, p0, fmaf(x1, p1, sx));
-          }
-        l += la;
-      }
     }
   };
 
