@@ -124,6 +124,33 @@ def test_sample_ties_at_the_top_p_cut(gpu):
     assert r["next"][0, 3].item() == 17 and r["next"][0, 4].item() == 0
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_sample_tiny_and_huge_logits(gpu, dtype):
+    """Rows of subnormal-range logits (the warper's product and quotient among
+    the subnormals), rows of logits in the thousands (the fp32 bound on L
+    widens with |m|), and a planted favourite among tiny values: every draw
+    bit-exact against the oracle."""
+    M, V = 6, 8195
+    g = torch.Generator().manual_seed(12)
+    base = torch.randn((1, M, V), generator=g)
+    tiny = 1e-39 if dtype == torch.bfloat16 else 1e-6  # subnormal in the dtype
+    lg = base.clone()
+    lg[0, 0] *= tiny
+    lg[0, 1] *= tiny
+    lg[0, 1, 77] = 3.0
+    lg[0, 2] *= 2000.0 if dtype == torch.bfloat16 else 300.0
+    lg[0, 3] = lg[0, 3] * 2.0 + (4000.0 if dtype == torch.bfloat16 else 500.0)
+    lg[0, 4] *= 40.0
+    lg = lg.to(dtype)
+    draft = torch.randint(0, V, (1, M), generator=g)
+    parent_ref = torch.tensor([[-1, 0, 1, 2, 3]])
+    pos = torch.arange(M)
+    for temperature, top_p, top_k in [(0.3, 1.0, 5), (0.7, 0.9, 0), (1.0, 0.5, 0), (1.3, 1.0, 40), (0.7, 0.95, 20)]:
+        print(f"[sample tiny/huge] {dtype} T={temperature} top_p={top_p} top_k={top_k}", flush=True)
+        run_and_compare(lg.to(gpu), draft.to(gpu), parent_ref.to(gpu), pos.to(gpu), 8, temperature, top_p, top_k,
+                        seed=41)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_sample_rows_with_infinite_logits(gpu, dtype):
     """Rows holding +inf logits (one, two tied, with NaNs beside), and f16 rows
