@@ -122,8 +122,21 @@ __global__ void __launch_bounds__(256) lse_merge_kernel(const MergeArgs a) {
   const int h = kvh * a.G + g;
   if (sg == 0) {
     const int64_t obase = (int64_t)b * a.o_sb + (int64_t)m * a.o_sm + (int64_t)h * a.o_sh + tc * 8;
+    if (a.out_dtype != 2 && ((reinterpret_cast<uintptr_t>(a.out) + 2 * obase) & 15) == 0) {
+      // 16-bit output, 16-byte aligned: the lane's 8 values in one store.
+      uint32_t w[4];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) store_val(a.out, a.out_dtype, obase + e, acc[e] * invL);
+      for (int e = 0; e < 4; ++e) {
+        const float x0 = acc[2 * e] * invL, x1 = acc[2 * e + 1] * invL;
+        w[e] = a.out_dtype == 0
+                   ? ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x0) | ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x1) << 16))
+                   : ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x0) | ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x1) << 16));
+      }
+      *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(a.out) + obase) = u32x4{w[0], w[1], w[2], w[3]};
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) store_val(a.out, a.out_dtype, obase + e, acc[e] * invL);
+    }
   }
   if (lane == 0) {
     const float lse = (L > 0.f) ? (mrun + __log2f(L)) * kLn2 : kNegInf;
