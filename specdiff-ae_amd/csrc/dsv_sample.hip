@@ -42,13 +42,17 @@
 //       the draw are taken when it fits; otherwise the bound comes from index
 //       passes over the row and the sweep draws.
 //   sample_sweep_kernel   one workgroup per (row, vocabulary range) of the
-//       rows still open (all rows without top-p / top-k):
+//       rows still open (rows without top-p / top-k when the logits are f32):
 //       the Gumbel-max draw over the range's kept entries.  Against a
 //       wave-shared lower bound lb of the range's maximum z, an entry whose
 //       1 - U exceeds an upper bound of e^(y - lb) cannot reach lb (one 2^x
 //       per entry from x * fl(1/T)); the few others take the exact warper,
 //       the keep test and an fp32 estimate of z (within 2^-14 of it), which
 //       leaves the exact double evaluation to the entries that can still win.
+//   sample_temp_kernel    temperature alone with 16-bit logits: one workgroup
+//       per row; the maximum entry's exact z bounds the row's maximum z from
+//       the start, and the groups that can still reach the bound are queued
+//       per wave and drawn 64 at a time (the sweep's screen and draw).
 //   the walk of dsv_accept.hip combines the ranges' draws and walks.
 
 #include "dsv_internal.h"
@@ -1526,6 +1530,196 @@ __global__ void __launch_bounds__(kSweepThreads) sample_sweep_kernel(const Accep
   }
 }
 
+// Temperature alone, 16-bit logits: one workgroup per row.  Pass 1 finds the
+// row maximum and an entry that holds it; that entry's exact z (it is kept,
+// as every finite entry is) is a lower bound of the row's maximum z from the
+// start, for every wave.  Pass 2 screens each group of four against the
+// bound without the generator (G < kGumbelMax) and queues the groups that
+// pass per wave in LDS; they are drawn 64 at a time, one per lane, with the
+// sweep's screen, estimate and exact draw.  Rows holding NaN start from no
+// bound.
+constexpr int kTempThreads = 512;
+
+template <typename LT>
+__global__ void __launch_bounds__(kTempThreads) __attribute__((amdgpu_waves_per_eu(4))) sample_temp_kernel(const AcceptArgs a) {
+  static_assert(sizeof(LT) == 2, "16-bit logits");
+  constexpr int NV = 8, kWv = kTempThreads / 64;
+  const int64_t row = blockIdx.x;
+  const int t = (int)(row / a.M), i = (int)(row % a.M);
+  const LT* x = reinterpret_cast<const LT*>(a.logits) + (int64_t)t * a.l_st + (int64_t)i * a.l_sm;
+  const int64_t V = a.V;
+  const Warp wp = make_warp(a.temperature);
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const uint32_t k0 = (uint32_t)a.seed, k1 = (uint32_t)(a.seed >> 32);
+  __shared__ float red_v[kWv];
+  __shared__ int64_t red_p[kWv];
+  __shared__ uint32_t red_n[kWv];
+  __shared__ float lb0_s;
+  __shared__ uint4 qbuf[kWv][64 * (NV / 4 + 1)];
+  __shared__ double sb[kWv];
+  __shared__ int si[kWv];
+
+  // ---- pass 1: the maximum of the logits (a thread's running maximum and the
+  // vector where it first occurred), NaN noted ------------------------------------
+  float xm = kNegInfF;
+  int64_t xp = -1;
+  uint32_t nan_seen = 0;
+  row_sweep<LT, kTempThreads, false, true>(x, 0, V, wp, [&](int64_t v0, const float(&xv)[NV]) {
+    float vm = xv[0];
+#pragma unroll
+    for (int e = 1; e < NV; ++e) vm = __builtin_elementwise_maximum(vm, xv[e]);  // NaN propagates
+    nan_seen |= vm != vm ? 1u : 0u;
+    if (vm > xm) {
+      xm = vm;
+      xp = v0;
+    }
+  });
+  float bv = xm;
+  int64_t bp = xp;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o);
+    const int64_t op = __shfl_xor(bp, o);
+    if (ov > bv || (ov == bv && op >= 0 && (bp < 0 || op < bp))) {
+      bv = ov;
+      bp = op;
+    }
+    nan_seen |= __shfl_xor(nan_seen, o);
+  }
+  if (lane == 0) {
+    red_v[wv] = bv;
+    red_p[wv] = bp;
+    red_n[wv] = nan_seen;
+  }
+  __syncthreads();
+  double best = -__builtin_huge_val();
+  int bi = -1;
+  if (tid == 0) {
+    float gv = red_v[0];
+    int64_t gp = red_p[0];
+    uint32_t gn = red_n[0];
+    for (int w = 1; w < kWv; ++w) {
+      if (red_v[w] > gv || (red_v[w] == gv && red_p[w] >= 0 && (gp < 0 || red_p[w] < gp))) {
+        gv = red_v[w];
+        gp = red_p[w];
+      }
+      gn |= red_n[w];
+    }
+    float lb0 = kNegInfF;
+    int e = -1;  // an entry of vector gp that holds the maximum
+    if (gn == 0u && gv > kNegInfF && gp >= 0)
+      for (int q = 0; q < NV && e < 0; ++q)
+        if (gp + q < V && raw_to_f<LT>(x[gp + q]) == gv) e = q;
+    if (e >= 0) {
+      // Its exact z.
+      const int64_t v = gp + e;
+      const float yv = warp_yf<LT>(gv, wp);
+      const double z = (double)yv + gumbel(draw_word(v, i, t, a.seed));
+      best = z;
+      bi = (int)v;
+      // A float at or below z (z rounded to nearest is within half an ulp).
+      lb0 = (float)z;
+      if ((double)lb0 > z) lb0 = lb0 - fabsf(lb0) * 0x1p-23f - 0x1p-126f;
+    }
+    lb0_s = lb0;
+  }
+  __syncthreads();
+
+  // ---- pass 2: the groups that can reach the bound, queued and drawn ---------------
+  float lb = lb0_s, lbl = kNegInfF;
+  auto group = [&](int64_t g, const float (&x4)[4], bool& upd) {
+    const uint4 w4 = philox4x32((uint32_t)(g >> 2), (uint32_t)i, (uint32_t)t, 0u, k0, k1);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t w = word_of(w4, e);
+      const float ya = x4[e] * wp.rT;
+      float yh = fmaf(fabsf(ya), 0x1p-7f, ya);  // NaN for x = -inf or NaN: screened exactly
+      if constexpr (__is_same(LT, _Float16)) yh = yh >= 65520.f ? __builtin_huge_valf() : yh;
+      // The sweep kernel's screen: 1 - U <= -ln U (see there).
+      const float tq = __builtin_amdgcn_exp2f(fmaf(yh - lb, 0x1.715476p+0f, 32.f + 0x1p-9f));
+      if ((float)(~w) > tq) continue;
+      const float yy = warp_yf<LT>(x4[e], wp);
+      if (!(yy > kNegInfF)) continue;
+      const float zf = yy + gumbel_est(w);
+      const float mg = kZMargin + fabsf(zf) * kZMarginRel;
+      lbl = fmaxf(lbl, zf - mg);
+      upd = true;
+      if (zf + mg >= lb) {
+        const double z = (double)yy + gumbel(w);
+        if (bi < 0 || z > best || (z == best && (int)(g + e) < bi)) {
+          best = z;
+          bi = (int)(g + e);
+        }
+      }
+    }
+  };
+  uint4* qw = qbuf[wv];
+  uint32_t qn = 0;  // queued groups (the same in every lane)
+  auto drain = [&](uint32_t n) {  // groups [0, n), one per lane
+    for (uint32_t s0 = 0; s0 < n; s0 += 64) {
+      bool upd = false;
+      if (s0 + (uint32_t)lane < n) {
+        const uint4 it = qw[s0 + lane];
+        const float x4[4] = {raw_to_f<LT>(__builtin_bit_cast(LT, (uint16_t)(it.y & 0xFFFFu))),
+                             raw_to_f<LT>(__builtin_bit_cast(LT, (uint16_t)(it.y >> 16))),
+                             raw_to_f<LT>(__builtin_bit_cast(LT, (uint16_t)(it.z & 0xFFFFu))),
+                             raw_to_f<LT>(__builtin_bit_cast(LT, (uint16_t)(it.z >> 16)))};
+        group((int64_t)it.x, x4, upd);
+      }
+      if (__ballot(upd) != 0ull) {
+        float wl = lbl;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) wl = fmaxf(wl, __shfl_xor(wl, o));
+        lb = fmaxf(lb, wl);
+      }
+    }
+  };
+  row_sweep<LT, kTempThreads, false, true>(x, 0, V, wp, [&](int64_t v0, const float(&xv)[NV]) {
+#pragma unroll
+    for (int gq = 0; gq < NV / 4; ++gq) {
+      float ym = kNegInfF;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float ya = xv[4 * gq + e] * wp.rT;
+        float h = fmaf(fabsf(ya), 0x1p-7f, ya);
+        if constexpr (__is_same(LT, _Float16)) h = h >= 65520.f ? __builtin_huge_valf() : h;
+        ym = fmaxf(ym, h);
+      }
+      // G < kGumbelMax: a group whose largest y cannot reach the bound holds no winner.
+      const bool pass = ym + kGumbelMax >= lb;
+      const uint64_t bal = __ballot(pass);
+      if (bal != 0ull) {
+        if (pass) {
+          uint32_t b[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) b[e] = (uint32_t)__builtin_bit_cast(uint16_t, f_to_raw<LT>(xv[4 * gq + e]));
+          qw[qn + (uint32_t)__popcll(bal & ((1ull << lane) - 1ull))] =
+              make_uint4((uint32_t)(v0 + 4 * gq), b[0] | (b[1] << 16), b[2] | (b[3] << 16), 0u);
+        }
+        qn += (uint32_t)__popcll(bal);
+      }
+    }
+    if (qn >= 64u) {
+      const uint32_t full = qn & ~63u, rest = qn - full;
+      drain(full);
+      // The rest (fewer than 64, at positions 64 and above) to the front.
+      uint4 it = make_uint4(0u, 0u, 0u, 0u);
+      if ((uint32_t)lane < rest) it = qw[full + lane];
+      if ((uint32_t)lane < rest) qw[lane] = it;
+      qn = rest;
+    }
+  });
+  drain(qn);
+  block_argmax(best, bi, sb, si, kTempThreads);
+  if (tid == 0) {
+    const uint64_t zb = __builtin_bit_cast(uint64_t, best);
+    for (int c = 0; c < a.nchunk; ++c)
+      a.rstat[row * a.nchunk + c] =
+          c == 0 ? make_float4(__uint_as_float((uint32_t)zb), __uint_as_float((uint32_t)(zb >> 32)), __int_as_float(bi), 0.f)
+                 : make_float4(0.f, 0.f, __int_as_float(-1), 0.f);
+  }
+}
+
 template <typename LT>
 hipError_t launch_sample_t(const AcceptArgs& a, hipStream_t s) {
   const unsigned rows = (unsigned)((int64_t)a.T * a.M);
@@ -1541,6 +1735,12 @@ hipError_t launch_sample_t(const AcceptArgs& a, hipStream_t s) {
     hipLaunchKernelGGL(sample_radix_kernel<LT>, dim3(rows), dim3(kRadixThreads), 0, s, a);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
+  }
+  if constexpr (sizeof(LT) == 2) {
+    if (a.sel == nullptr) {  // temperature alone
+      hipLaunchKernelGGL(sample_temp_kernel<LT>, dim3(rows), dim3(kTempThreads), 0, s, a);
+      return hipGetLastError();
+    }
   }
   hipLaunchKernelGGL(sample_sweep_kernel<LT>, dim3((unsigned)a.nchunk, rows), dim3(kSweepThreads), 0, s, a);
   return hipGetLastError();
