@@ -682,7 +682,7 @@ __device__ __forceinline__ float x_threshold(float thr, const Warp& w) {
 // < kTheta[j], bin 16 the rest (and NaN).
 constexpr int kBins = kNTheta + 1;
 // The statistics pass also keeps, per wave, the entries with a >= -g in a
-// region of kCap / waves entries: g starts at kPreG0 and drops by 2 (the
+// region of kPre / waves entries: g starts at kPreG0 and drops by 2 (the
 // region compacted) whenever the region would overflow, down to kPreGMin.
 // a is the same fp32 expression wherever it is evaluated, and monotone in y,
 // so {a >= -theta} is a head of the order, held by the regions when theta <=
@@ -707,9 +707,10 @@ __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) sa
   const Warp wp = make_warp(a.temperature);
   constexpr int NV = 16 / sizeof(LT);
 
-  // hist: the per-lane histograms of the statistics pass, then the head's
-  // candidates ((key << 32) | index).  pre: the waves' regions of entries near
-  // the maximum, (index << 32) | bits of y.
+  // hist: the per-lane histograms of the histogram pass (rows whose regions
+  // do not hold the cut), and the head's candidates ((key << 32) | index).
+  // pre: the waves' regions of entries near the maximum, (index << 32) | bits
+  // of y.
   __shared__ __align__(16) uint32_t hist[kHistWords];
   __shared__ __align__(16) uint64_t pre[kPre];
   uint64_t* cand = reinterpret_cast<uint64_t*>(hist);
