@@ -647,13 +647,13 @@ __device__ __forceinline__ void warp_vec_raw(float (&y)[N], const Warp& w) {
   }
 }
 
-// The smallest logit x (in the dtype's order, NaN excluded) whose warped y is
-// at least thr; thr is finite, so +inf qualifies.  The warper is monotone,
-// so {x : y(x) >= thr} = {x >= result}.  Wave-parallel search over the order
-// keys: each round the 64 lanes test 64 evenly spaced keys.  Every lane of
-// the wave calls it and gets the result.
+// The bits of the smallest logit x (in the dtype's order, NaN excluded) whose
+// warped y is at least thr; thr is not NaN, so +inf qualifies.  The warper
+// is monotone, so {x : y(x) >= thr} = {x >= result}.  Wave-parallel search
+// over the order keys: each round the 64 lanes test 64 evenly spaced keys.
+// Every lane of the wave calls it and gets the result.
 template <typename LT>
-__device__ __forceinline__ float x_threshold(float thr, const Warp& w) {
+__device__ __forceinline__ uint32_t x_threshold_bits(float thr, const Warp& w) {
   constexpr bool k16 = sizeof(LT) == 2;
   const uint32_t sign = k16 ? 0x8000u : 0x80000000u, all = k16 ? 0xFFFFu : 0xFFFFFFFFu;
   const uint32_t inf = (uint32_t)IntOrder<LT>::kInf, ninf = ((uint32_t)IntOrder<LT>::kNegInf) & all;
@@ -674,7 +674,11 @@ __device__ __forceinline__ float x_threshold(float thr, const Warp& w) {
     lo = l == 0 ? lo : lo + (uint64_t)l * step;
     hi = nhi;
   }
-  return int_to_f<LT>((int)bits_of((uint32_t)lo));
+  return bits_of((uint32_t)lo);
+}
+template <typename LT>
+__device__ __forceinline__ float x_threshold(float thr, const Warp& w) {
+  return int_to_f<LT>((int)x_threshold_bits<LT>(thr, w));
 }
 
 // Histogram bins of a = (y - m) log2 e, read off |a|'s bits (exponent and first
@@ -1531,19 +1535,87 @@ __global__ void __launch_bounds__(kSweepThreads) sample_sweep_kernel(const Accep
   }
 }
 
-// Temperature alone, 16-bit logits: one workgroup per row.  Pass 1 finds the
-// row maximum and an entry that holds it; that entry's exact z (it is kept,
-// as every finite entry is) is a lower bound of the row's maximum z from the
-// start, for every wave.  Pass 2 screens each group of four against the
-// bound without the generator (G < kGumbelMax) and queues the groups that
-// pass per wave in LDS; they are drawn 64 at a time, one per lane, with the
-// sweep's screen, estimate and exact draw.  Rows holding NaN start from no
-// bound.
+// The 16-byte vector of 16-bit logits at v0 as loaded; entries at or past hi
+// read as -inf.
+template <typename LT>
+__device__ __forceinline__ u32x4 load_words(const LT* x, int64_t v0, int64_t hi, bool aligned) {
+  static_assert(sizeof(LT) == 2, "16-bit logits");
+  if (aligned && v0 + 8 <= hi) return *reinterpret_cast<const u32x4*>(x + v0);
+  constexpr uint32_t ninf = (uint32_t)IntOrder<LT>::kNegInf & 0xFFFFu;
+  uint32_t w[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t lo = v0 + 2 * e < hi ? (uint32_t)__builtin_bit_cast(uint16_t, x[v0 + 2 * e]) : ninf;
+    const uint32_t up = v0 + 2 * e + 1 < hi ? (uint32_t)__builtin_bit_cast(uint16_t, x[v0 + 2 * e + 1]) : ninf;
+    w[e] = lo | (up << 16);
+  }
+  return u32x4{w[0], w[1], w[2], w[3]};
+}
+
+// row_sweep's order and loads over [lo, hi) (16-bit logits), handing f(v0, r)
+// the vector's words as loaded instead of floats.
+template <typename LT, int NT, typename F>
+__device__ __forceinline__ void row_sweep_words(const LT* x, int64_t lo, int64_t hi, F&& f) {
+  constexpr int N = 8;
+  constexpr int64_t kStep = (int64_t)2 * NT * N;
+  constexpr int64_t kSpan = (int64_t)(NT + 64) * N;  // a wave's two vectors lie in [b0, b0 + kSpan)
+  const bool aligned = (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+  const int lane = threadIdx.x & 63;
+  int64_t b0 = lo + (int64_t)(threadIdx.x & ~63) * N;  // uniform over the wave
+  if (aligned && b0 + kSpan <= hi) {
+    const LT* p = x + b0 + (int64_t)lane * N;
+    u32x4 ra = *reinterpret_cast<const u32x4*>(p), rb = *reinterpret_cast<const u32x4*>(p + NT * N);
+    for (;;) {
+      const bool more = b0 + kStep + kSpan <= hi;  // uniform over the wave
+      u32x4 na, nb;
+      if (more) {
+        na = *reinterpret_cast<const u32x4*>(p + kStep);
+        nb = *reinterpret_cast<const u32x4*>(p + kStep + NT * N);
+      }
+      f(b0 + (int64_t)lane * N, ra);
+      f(b0 + (int64_t)lane * N + (int64_t)NT * N, rb);
+      b0 += kStep;
+      p += kStep;
+      if (!more) break;
+      ra = na;
+      rb = nb;
+    }
+  }
+  for (; b0 < hi; b0 += kStep) {
+    const int64_t v0 = b0 + (int64_t)lane * N, v1 = v0 + (int64_t)NT * N;
+    const u32x4 ra = load_words<LT>(x, v0, hi, aligned), rb = load_words<LT>(x, v1, hi, aligned);
+    f(v0, ra);
+    f(v1, rb);
+  }
+}
+
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+// Temperature alone, 16-bit logits: one workgroup per row, or up to 8 when
+// the rows are few, each drawing over a run of the row's vocabulary ranges.
+// Pass 1 (over the whole row, in every workgroup) takes packed signed 16-bit extremes of the logits' bits: among
+// non-negative bits the integer order is the float order, among negative
+// bits the reverse, so the largest non-negative integer is the largest
+// logit when there is one, else the smallest integer is.  Each half of a
+// thread's running maximum and minimum keeps the vector where it last
+// changed, so the row's largest logit comes with a vector that holds it; that
+// entry's exact z (it is kept, as every finite entry is) bounds the row's
+// maximum z from below (lb) from the start, for every wave.  Positive NaNs
+// never stand for the maximum (a thread that met one offers only its
+// negative side); any entry found is a valid bound.
+// Pass 2 keeps a group of four only if one of its logits x has
+// y(x) >= lb - kGumbelMax (as G < kGumbelMax), tested on the bits against the
+// smallest such logit xt (the warper is monotone): i16(h) >= i16(xt) for a
+// non-negative xt, else u16(h) <= u16(xt); negative NaNs never pass.  The
+// groups kept are queued per wave in LDS and drawn 64 at a time, one per
+// lane, with the sweep's screen, estimate and exact draw.  xt is recomputed
+// when lb has risen by 4 (a lower xt only keeps more groups).
 constexpr int kTempThreads = 512;
 
 template <typename LT>
 __global__ void __launch_bounds__(kTempThreads) __attribute__((amdgpu_waves_per_eu(4))) sample_temp_kernel(const AcceptArgs a) {
   static_assert(sizeof(LT) == 2, "16-bit logits");
+  using IO = IntOrder<LT>;
   constexpr int NV = 8, kWv = kTempThreads / 64;
   const int64_t row = blockIdx.x;
   const int t = (int)(row / a.M), i = (int)(row % a.M);
@@ -1552,69 +1624,88 @@ __global__ void __launch_bounds__(kTempThreads) __attribute__((amdgpu_waves_per_
   const Warp wp = make_warp(a.temperature);
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const uint32_t k0 = (uint32_t)a.seed, k1 = (uint32_t)(a.seed >> 32);
-  __shared__ float red_v[kWv];
-  __shared__ int64_t red_p[kWv];
-  __shared__ uint32_t red_n[kWv];
+  // This workgroup's vocabulary ranges [c0, c1) of the row's a.nchunk: the
+  // row's gridDim.y workgroups take consecutive runs of G ranges.
+  const int G = (a.nchunk + (int)gridDim.y - 1) / (int)gridDim.y;
+  const int c0 = min((int)blockIdx.y * G, a.nchunk), c1 = min(c0 + G, a.nchunk);
+  const int64_t lo = (int64_t)c0 * a.chunk, hi = min(V, (int64_t)c1 * a.chunk);
+  __shared__ int red_k[kWv];
+  __shared__ int red_p[kWv];
   __shared__ float lb0_s;
   __shared__ uint4 qbuf[kWv][64 * (NV / 4 + 1)];
   __shared__ double sb[kWv];
   __shared__ int si[kWv];
 
-  // ---- pass 1: the maximum of the logits (a thread's running maximum and the
-  // vector where it first occurred), NaN noted ------------------------------------
-  float xm = kNegInfF;
-  int64_t xp = -1;
-  uint32_t nan_seen = 0;
-  row_sweep<LT, kTempThreads, false, true>(x, 0, V, wp, [&](int64_t v0, const float(&xv)[NV]) {
-    float vm = xv[0];
+  // ---- pass 1: the largest logit and a vector that holds it ------------------------
+  s16x2 pmax = {(short)-32768, (short)-32768}, nmin = {(short)32767, (short)32767};
+  int px = -1, py = -1, nx = -1, ny = -1;
+  row_sweep_words<LT, kTempThreads>(x, 0, V, [&](int64_t v0, const u32x4& r) {
+    s16x2 s[4];
 #pragma unroll
-    for (int e = 1; e < NV; ++e) vm = __builtin_elementwise_maximum(vm, xv[e]);  // NaN propagates
-    nan_seen |= vm != vm ? 1u : 0u;
-    if (vm > xm) {
-      xm = vm;
-      xp = v0;
+    for (int w = 0; w < 4; ++w) {
+      const uint32_t rw = r[w];  // (a bit cast of the element itself reads element 0)
+      s[w] = __builtin_bit_cast(s16x2, rw);
     }
+    const s16x2 vmax = __builtin_elementwise_max(__builtin_elementwise_max(s[0], s[1]), __builtin_elementwise_max(s[2], s[3]));
+    const s16x2 vmin = __builtin_elementwise_min(__builtin_elementwise_min(s[0], s[1]), __builtin_elementwise_min(s[2], s[3]));
+    const s16x2 pn = __builtin_elementwise_max(pmax, vmax), nn = __builtin_elementwise_min(nmin, vmin);
+    if (pn.x != pmax.x) px = (int)v0;
+    if (pn.y != pmax.y) py = (int)v0;
+    if (nn.x != nmin.x) nx = (int)v0;
+    if (nn.y != nmin.y) ny = (int)v0;
+    pmax = pn;
+    nmin = nn;
   });
-  float bv = xm;
-  int64_t bp = xp;
+  // The thread's candidate as one ordered key: 0x10000 + bits for a
+  // non-negative logit, -i16(bits) for a negative one (-inf included), -1 for
+  // none.
+  int key = -1, kp = -1;
+  {
+    const int hm = pmax.x >= pmax.y ? (int)pmax.x : (int)pmax.y;
+    const int hp = pmax.x >= pmax.y ? px : py;
+    const int hn = nmin.x <= nmin.y ? (int)nmin.x : (int)nmin.y;
+    const int hq = nmin.x <= nmin.y ? nx : ny;
+    if (hm >= 0 && hm <= IO::kInf) {
+      key = 0x10000 + hm;
+      kp = hp;
+    } else if (hn <= IO::kNegInf) {
+      key = -hn;
+      kp = hq;
+    }
+  }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
-    const float ov = __shfl_xor(bv, o);
-    const int64_t op = __shfl_xor(bp, o);
-    if (ov > bv || (ov == bv && op >= 0 && (bp < 0 || op < bp))) {
-      bv = ov;
-      bp = op;
+    const int ok = __shfl_xor(key, o), op = __shfl_xor(kp, o);
+    if (ok > key || (ok == key && op < kp)) {
+      key = ok;
+      kp = op;
     }
-    nan_seen |= __shfl_xor(nan_seen, o);
   }
   if (lane == 0) {
-    red_v[wv] = bv;
-    red_p[wv] = bp;
-    red_n[wv] = nan_seen;
+    red_k[wv] = key;
+    red_p[wv] = kp;
   }
   __syncthreads();
   double best = -__builtin_huge_val();
   int bi = -1;
   if (tid == 0) {
-    float gv = red_v[0];
-    int64_t gp = red_p[0];
-    uint32_t gn = red_n[0];
-    for (int w = 1; w < kWv; ++w) {
-      if (red_v[w] > gv || (red_v[w] == gv && red_p[w] >= 0 && (gp < 0 || red_p[w] < gp))) {
-        gv = red_v[w];
+    int gk = red_k[0], gp = red_p[0];
+    for (int w = 1; w < kWv; ++w)
+      if (red_k[w] > gk || (red_k[w] == gk && red_p[w] < gp)) {
+        gk = red_k[w];
         gp = red_p[w];
       }
-      gn |= red_n[w];
-    }
     float lb0 = kNegInfF;
-    int e = -1;  // an entry of vector gp that holds the maximum
-    if (gn == 0u && gv > kNegInfF && gp >= 0)
+    int e = -1;  // an entry of vector gp with those bits
+    if (gk >= 0 && gp >= 0) {
+      const uint32_t bits = gk >= 0x10000 ? (uint32_t)(gk - 0x10000) : ((uint32_t)(-gk) & 0xFFFFu);
       for (int q = 0; q < NV && e < 0; ++q)
-        if (gp + q < V && raw_to_f<LT>(x[gp + q]) == gv) e = q;
+        if (gp + q < V && (uint32_t)__builtin_bit_cast(uint16_t, x[gp + q]) == bits) e = q;
+    }
     if (e >= 0) {
       // Its exact z.
       const int64_t v = gp + e;
-      const float yv = warp_yf<LT>(gv, wp);
+      const float yv = warp_y<LT>(x[v], wp);
       const double z = (double)yv + gumbel(draw_word(v, i, t, a.seed));
       best = z;
       bi = (int)v;
@@ -1628,6 +1719,29 @@ __global__ void __launch_bounds__(kTempThreads) __attribute__((amdgpu_waves_per_
 
   // ---- pass 2: the groups that can reach the bound, queued and drawn ---------------
   float lb = lb0_s, lbl = kNegInfF;
+  // The screen (uniform over the wave): tneg and the packed operand tpk,
+  // u16(xt) + 1 or i16(xt) - 1 in both halves, for the lb of lb_t.
+  int tneg = 1;
+  uint32_t tpk = 0;
+  float lb_t = kNegInfF;
+  auto set_threshold = [&]() {
+    // At most lb - kGumbelMax: the two roundings are within 2^-23 |lb|.
+    const float thr = (lb > kNegInfF && lb < -kNegInfF) ? (lb - kGumbelMax) - fabsf(lb) * 0x1p-21f : lb;
+    const uint32_t xb = x_threshold_bits<LT>(thr, wp);
+    const bool neg = (xb & 0x8000u) != 0u;
+    const uint32_t c = (neg ? xb + 1u : xb - 1u) & 0xFFFFu;
+    tneg = __builtin_amdgcn_readfirstlane(neg ? 1 : 0);
+    tpk = __builtin_amdgcn_readfirstlane(c | (c << 16));
+    lb_t = lb;
+  };
+  auto screen = [&](uint32_t w0, uint32_t w1) -> bool {
+    if (tneg) {
+      const u16x2 m = __builtin_elementwise_min(__builtin_bit_cast(u16x2, w0), __builtin_bit_cast(u16x2, w1));
+      return __builtin_bit_cast(uint32_t, __builtin_elementwise_min(m, __builtin_bit_cast(u16x2, tpk))) != tpk;
+    }
+    const s16x2 m = __builtin_elementwise_max(__builtin_bit_cast(s16x2, w0), __builtin_bit_cast(s16x2, w1));
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(m, __builtin_bit_cast(s16x2, tpk))) != tpk;
+  };
   auto group = [&](int64_t g, const float (&x4)[4], bool& upd) {
     const uint4 w4 = philox4x32((uint32_t)(g >> 2), (uint32_t)i, (uint32_t)t, 0u, k0, k1);
 #pragma unroll
@@ -1675,28 +1789,16 @@ __global__ void __launch_bounds__(kTempThreads) __attribute__((amdgpu_waves_per_
       }
     }
   };
-  row_sweep<LT, kTempThreads, false, true>(x, 0, V, wp, [&](int64_t v0, const float(&xv)[NV]) {
+  set_threshold();
+  row_sweep_words<LT, kTempThreads>(x, lo, hi, [&](int64_t v0, const u32x4& r) {
 #pragma unroll
     for (int gq = 0; gq < NV / 4; ++gq) {
-      float ym = kNegInfF;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float ya = xv[4 * gq + e] * wp.rT;
-        float h = fmaf(fabsf(ya), 0x1p-7f, ya);
-        if constexpr (__is_same(LT, _Float16)) h = h >= 65520.f ? __builtin_huge_valf() : h;
-        ym = fmaxf(ym, h);
-      }
-      // G < kGumbelMax: a group whose largest y cannot reach the bound holds no winner.
-      const bool pass = ym + kGumbelMax >= lb;
+      const uint32_t w0 = r[2 * gq], w1 = r[2 * gq + 1];
+      const bool pass = screen(w0, w1);
       const uint64_t bal = __ballot(pass);
       if (bal != 0ull) {
-        if (pass) {
-          uint32_t b[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) b[e] = (uint32_t)__builtin_bit_cast(uint16_t, f_to_raw<LT>(xv[4 * gq + e]));
-          qw[qn + (uint32_t)__popcll(bal & ((1ull << lane) - 1ull))] =
-              make_uint4((uint32_t)(v0 + 4 * gq), b[0] | (b[1] << 16), b[2] | (b[3] << 16), 0u);
-        }
+        if (pass)
+          qw[qn + (uint32_t)__popcll(bal & ((1ull << lane) - 1ull))] = make_uint4((uint32_t)(v0 + 4 * gq), w0, w1, 0u);
         qn += (uint32_t)__popcll(bal);
       }
     }
@@ -1708,16 +1810,19 @@ __global__ void __launch_bounds__(kTempThreads) __attribute__((amdgpu_waves_per_
       if ((uint32_t)lane < rest) it = qw[full + lane];
       if ((uint32_t)lane < rest) qw[lane] = it;
       qn = rest;
+      if (lb > lb_t + 4.f) set_threshold();
     }
   });
   drain(qn);
   block_argmax(best, bi, sb, si, kTempThreads);
   if (tid == 0) {
+    // The draw over this workgroup's ranges (and the bound's entry, which
+    // every workgroup of the row may report) as range c0's result.
     const uint64_t zb = __builtin_bit_cast(uint64_t, best);
-    for (int c = 0; c < a.nchunk; ++c)
+    for (int c = c0; c < c1; ++c)
       a.rstat[row * a.nchunk + c] =
-          c == 0 ? make_float4(__uint_as_float((uint32_t)zb), __uint_as_float((uint32_t)(zb >> 32)), __int_as_float(bi), 0.f)
-                 : make_float4(0.f, 0.f, __int_as_float(-1), 0.f);
+          c == c0 ? make_float4(__uint_as_float((uint32_t)zb), __uint_as_float((uint32_t)(zb >> 32)), __int_as_float(bi), 0.f)
+                  : make_float4(0.f, 0.f, __int_as_float(-1), 0.f);
   }
 }
 
@@ -1739,7 +1844,16 @@ hipError_t launch_sample_t(const AcceptArgs& a, hipStream_t s) {
   }
   if constexpr (sizeof(LT) == 2) {
     if (a.sel == nullptr) {  // temperature alone
-      hipLaunchKernelGGL(sample_temp_kernel<LT>, dim3(rows), dim3(kTempThreads), 0, s, a);
+      // One workgroup per row when the rows fill the CUs twice, else up to 8
+      // per row, each on a run of the row's ranges (each one's pass 1 reads
+      // the whole row).
+      const int64_t cus = a.cus > 0 ? a.cus : 256;
+      int64_t wpr = 2 * cus / (int64_t)rows;
+      wpr = wpr < 1 ? 1 : (wpr > 8 ? 8 : wpr);
+      wpr = wpr > a.nchunk ? a.nchunk : wpr;
+      const int64_t G = (a.nchunk + wpr - 1) / wpr;
+      hipLaunchKernelGGL(sample_temp_kernel<LT>, dim3(rows, (unsigned)((a.nchunk + G - 1) / G)), dim3(kTempThreads), 0,
+                         s, a);
       return hipGetLastError();
     }
   }

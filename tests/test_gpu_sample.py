@@ -102,23 +102,31 @@ def test_sample_random_configurations(gpu):
         run_and_compare(lg, a.draft, a.parent_ref, a.pos, 8, temperature, top_p, top_k, seed)
 
 
-def test_sample_ties_at_the_top_p_cut(gpu):
-    """bf16 rows of a few repeated values, so the top-p cut falls inside a tie
-    group (kept: its highest indices) and top-k ties are all kept."""
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_sample_ties_at_the_top_p_cut(gpu, dtype):
+    """16-bit rows of a few repeated values, so the top-p cut falls inside a
+    tie group (kept: its highest indices) and top-k ties are all kept; with
+    rows whose largest logit is -0 or negative, rows of -inf and NaNs of both
+    signs, also drawn with temperature alone."""
     M, V = 8, 4099
     g = torch.Generator().manual_seed(5)
-    lg = torch.randint(-3, 3, (1, M, V), generator=g).float().to(torch.bfloat16)
+    lg = torch.randint(-3, 3, (1, M, V), generator=g).float().to(dtype)
+    lg[0, 2] = -lg[0, 2].abs()                      # at most -0
+    lg[0, 7] -= 10.0                                # all negative
     lg[0, 3] = float("-inf")
     lg[0, 3, 17] = 2.0                              # one finite logit
     lg[0, 4, :] = float("-inf")                     # none: token 0
     lg[0, 5, 100:200] = float("nan")                # NaN counts as -inf
-    snan = torch.tensor([0x7F81, -0x7F], dtype=torch.int16).view(torch.bfloat16)  # signalling NaNs, both signs
+    snan = torch.tensor([0x7F81, -0x7F], dtype=torch.int16).view(dtype)  # signalling NaNs, both signs
     lg[0, 6, 10], lg[0, 6, 4000] = snan[0], snan[1]
     draft = torch.randint(0, V, (1, M), generator=g)
     parent_ref = torch.tensor([[-1, 0, 1, 2, 3, 4, 5]])
     pos = torch.arange(M)
-    for top_p, top_k in [(0.3, 0), (0.77, 0), (0.5, 7), (1.0, 3)]:
-        run_and_compare(lg.to(gpu), draft.to(gpu), parent_ref.to(gpu), pos.to(gpu), 8, 1.0, top_p, top_k, seed=99)
+    for temperature, top_p, top_k in [(1.0, 0.3, 0), (1.0, 0.77, 0), (1.0, 0.5, 7), (1.0, 1.0, 3), (1.0, 1.0, 0),
+                                      (0.6, 1.0, 0)]:
+        print(f"[sample ties] {dtype} T={temperature} top_p={top_p} top_k={top_k}", flush=True)
+        run_and_compare(lg.to(gpu), draft.to(gpu), parent_ref.to(gpu), pos.to(gpu), 8, temperature, top_p, top_k,
+                        seed=99)
     r = tree_accept(lg.to(gpu), draft.to(gpu), parent_ref.to(gpu), pos.to(gpu), 8, mode="sample", top_p=0.9, seed=4,
                     return_next=True)
     assert r["next"][0, 3].item() == 17 and r["next"][0, 4].item() == 0
