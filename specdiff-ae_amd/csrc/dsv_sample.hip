@@ -42,16 +42,19 @@
 //       the draw are taken when it fits; otherwise the bound comes from index
 //       passes over the row and the sweep draws.
 //   sample_sweep_kernel   one workgroup per (row, vocabulary range) of the
-//       rows still open (rows without top-p / top-k when the logits are f32):
+//       rows still open (f32 rows without top-p / top-k when rows are fewer
+//       than CUs):
 //       the Gumbel-max draw over the range's kept entries.  Against a
 //       wave-shared lower bound lb of the range's maximum z, an entry whose
 //       1 - U exceeds an upper bound of e^(y - lb) cannot reach lb (one 2^x
 //       per entry from x * fl(1/T)); the few others take the exact warper,
 //       the keep test and an fp32 estimate of z (within 2^-14 of it), which
 //       leaves the exact double evaluation to the entries that can still win.
-//   sample_temp_kernel    temperature alone with 16-bit logits: one workgroup
-//       per row; the maximum entry's exact z bounds the row's maximum z from
-//       the start, and the groups that can still reach the bound are queued
+//   sample_temp_kernel    temperature alone (f32 logits: with at least as
+//       many rows as CUs): one workgroup per row, or up to 8 when rows are
+//       few; the maximum entry's exact z bounds the row's maximum z from the
+//       start, groups are screened on their raw bits against the smallest
+//       logit that can still reach the bound, and the groups kept are queued
 //       per wave and drawn 64 at a time (the sweep's screen and draw).
 //   the walk of dsv_accept.hip combines the ranges' draws and walks.
 
@@ -1535,28 +1538,34 @@ __global__ void __launch_bounds__(kSweepThreads) sample_sweep_kernel(const Accep
   }
 }
 
-// The 16-byte vector of 16-bit logits at v0 as loaded; entries at or past hi
-// read as -inf.
+// The 16-byte vector of logits at v0 as loaded; entries at or past hi read
+// as -inf.
 template <typename LT>
 __device__ __forceinline__ u32x4 load_words(const LT* x, int64_t v0, int64_t hi, bool aligned) {
-  static_assert(sizeof(LT) == 2, "16-bit logits");
-  if (aligned && v0 + 8 <= hi) return *reinterpret_cast<const u32x4*>(x + v0);
-  constexpr uint32_t ninf = (uint32_t)IntOrder<LT>::kNegInf & 0xFFFFu;
+  constexpr int N = 16 / sizeof(LT);
+  if (aligned && v0 + N <= hi) return *reinterpret_cast<const u32x4*>(x + v0);
   uint32_t w[4];
+  if constexpr (sizeof(LT) == 4) {
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const uint32_t lo = v0 + 2 * e < hi ? (uint32_t)__builtin_bit_cast(uint16_t, x[v0 + 2 * e]) : ninf;
-    const uint32_t up = v0 + 2 * e + 1 < hi ? (uint32_t)__builtin_bit_cast(uint16_t, x[v0 + 2 * e + 1]) : ninf;
-    w[e] = lo | (up << 16);
+    for (int e = 0; e < 4; ++e)
+      w[e] = v0 + e < hi ? __builtin_bit_cast(uint32_t, x[v0 + e]) : (uint32_t)IntOrder<LT>::kNegInf;
+  } else {
+    constexpr uint32_t ninf = (uint32_t)IntOrder<LT>::kNegInf & 0xFFFFu;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t lo = v0 + 2 * e < hi ? (uint32_t)__builtin_bit_cast(uint16_t, x[v0 + 2 * e]) : ninf;
+      const uint32_t up = v0 + 2 * e + 1 < hi ? (uint32_t)__builtin_bit_cast(uint16_t, x[v0 + 2 * e + 1]) : ninf;
+      w[e] = lo | (up << 16);
+    }
   }
   return u32x4{w[0], w[1], w[2], w[3]};
 }
 
-// row_sweep's order and loads over [lo, hi) (16-bit logits), handing f(v0, r)
-// the vector's words as loaded instead of floats.
+// row_sweep's order and loads over [lo, hi), handing f(v0, r) the vector's
+// words as loaded instead of floats.
 template <typename LT, int NT, typename F>
 __device__ __forceinline__ void row_sweep_words(const LT* x, int64_t lo, int64_t hi, F&& f) {
-  constexpr int N = 8;
+  constexpr int N = 16 / sizeof(LT);
   constexpr int64_t kStep = (int64_t)2 * NT * N;
   constexpr int64_t kSpan = (int64_t)(NT + 64) * N;  // a wave's two vectors lie in [b0, b0 + kSpan)
   const bool aligned = (reinterpret_cast<uintptr_t>(x) & 15) == 0;
@@ -1591,32 +1600,35 @@ __device__ __forceinline__ void row_sweep_words(const LT* x, int64_t lo, int64_t
 
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
-// Temperature alone, 16-bit logits: one workgroup per row, or up to 8 when
-// the rows are few, each drawing over a run of the row's vocabulary ranges.
-// Pass 1 (over the whole row, in every workgroup) takes packed signed 16-bit extremes of the logits' bits: among
+// Temperature alone: one workgroup per row, or up to 8 when the rows are
+// few, each drawing over a run of the row's vocabulary ranges.
+// Pass 1 (over the whole row, in every workgroup) takes signed integer
+// extremes of the logits' bits (packed 16-bit ones for 16-bit logits): among
 // non-negative bits the integer order is the float order, among negative
 // bits the reverse, so the largest non-negative integer is the largest
-// logit when there is one, else the smallest integer is.  Each half of a
-// thread's running maximum and minimum keeps the vector where it last
+// logit when there is one, else the smallest integer is.  Each extreme (each
+// half of a packed one) of a thread keeps the vector where it last
 // changed, so the row's largest logit comes with a vector that holds it; that
 // entry's exact z (it is kept, as every finite entry is) bounds the row's
 // maximum z from below (lb) from the start, for every wave.  Positive NaNs
 // never stand for the maximum (a thread that met one offers only its
 // negative side); any entry found is a valid bound.
 // Pass 2 keeps a group of four only if one of its logits x has
-// y(x) >= lb - kGumbelMax (as G < kGumbelMax), tested on the bits against the
-// smallest such logit xt (the warper is monotone): i16(h) >= i16(xt) for a
-// non-negative xt, else u16(h) <= u16(xt); negative NaNs never pass.  The
-// groups kept are queued per wave in LDS and drawn 64 at a time, one per
-// lane, with the sweep's screen, estimate and exact draw.  xt is recomputed
+// y(x) >= lb - kGumbelMax (as G < kGumbelMax), tested on the bits h against
+// the smallest such logit xt (the warper is monotone): int(h) >= int(xt) for
+// a non-negative xt, else uint(h) <= uint(xt), at the dtype's width; negative
+// NaNs never pass.  The groups kept are queued per wave in LDS (index and
+// raw words) and drawn 64 at a time, one per lane, with the sweep's screen,
+// estimate and exact draw.  xt is recomputed
 // when lb has risen by 4 (a lower xt only keeps more groups).
 constexpr int kTempThreads = 512;
 
 template <typename LT>
 __global__ void __launch_bounds__(kTempThreads) __attribute__((amdgpu_waves_per_eu(4))) sample_temp_kernel(const AcceptArgs a) {
-  static_assert(sizeof(LT) == 2, "16-bit logits");
   using IO = IntOrder<LT>;
-  constexpr int NV = 8, kWv = kTempThreads / 64;
+  constexpr bool k32 = sizeof(LT) == 4;
+  constexpr int NV = 16 / sizeof(LT), kGV = NV / 4, kWv = kTempThreads / 64;
+  constexpr int kQ = 64 * (kGV + 1);  // queue entries per wave
   const int64_t row = blockIdx.x;
   const int t = (int)(row / a.M), i = (int)(row % a.M);
   const LT* x = reinterpret_cast<const LT*>(a.logits) + (int64_t)t * a.l_st + (int64_t)i * a.l_sm;
@@ -1629,53 +1641,78 @@ __global__ void __launch_bounds__(kTempThreads) __attribute__((amdgpu_waves_per_
   const int G = (a.nchunk + (int)gridDim.y - 1) / (int)gridDim.y;
   const int c0 = min((int)blockIdx.y * G, a.nchunk), c1 = min(c0 + G, a.nchunk);
   const int64_t lo = (int64_t)c0 * a.chunk, hi = min(V, (int64_t)c1 * a.chunk);
-  __shared__ int red_k[kWv];
+  __shared__ int64_t red_k[kWv];
   __shared__ int red_p[kWv];
   __shared__ float lb0_s;
-  __shared__ uint4 qbuf[kWv][64 * (NV / 4 + 1)];
+  __shared__ uint4 qbuf[kWv][kQ];              // 16-bit: (index, words); 32-bit: the words
+  __shared__ uint32_t qidx[kWv][k32 ? kQ : 1];  // 32-bit: the index
   __shared__ double sb[kWv];
   __shared__ int si[kWv];
 
   // ---- pass 1: the largest logit and a vector that holds it ------------------------
-  s16x2 pmax = {(short)-32768, (short)-32768}, nmin = {(short)32767, (short)32767};
-  int px = -1, py = -1, nx = -1, ny = -1;
-  row_sweep_words<LT, kTempThreads>(x, 0, V, [&](int64_t v0, const u32x4& r) {
-    s16x2 s[4];
+  // hm, hn: the thread's largest and smallest integer (of the bits), at the
+  // vectors hp, hq.
+  int hm, hn, hp, hq;
+  if constexpr (k32) {
+    int pmax = INT32_MIN, nmin = INT32_MAX, pp = -1, np = -1;
+    row_sweep_words<LT, kTempThreads>(x, 0, V, [&](int64_t v0, const u32x4& r) {
+      const uint32_t a0 = r[0], a1 = r[1], a2 = r[2], a3 = r[3];
+      const int vmax = max(max((int)a0, (int)a1), max((int)a2, (int)a3));
+      const int vmin = min(min((int)a0, (int)a1), min((int)a2, (int)a3));
+      if (vmax > pmax) {
+        pmax = vmax;
+        pp = (int)v0;
+      }
+      if (vmin < nmin) {
+        nmin = vmin;
+        np = (int)v0;
+      }
+    });
+    hm = pmax;
+    hp = pp;
+    hn = nmin;
+    hq = np;
+  } else {
+    s16x2 pmax = {(short)-32768, (short)-32768}, nmin = {(short)32767, (short)32767};
+    int px = -1, py = -1, nx = -1, ny = -1;
+    row_sweep_words<LT, kTempThreads>(x, 0, V, [&](int64_t v0, const u32x4& r) {
+      s16x2 s[4];
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const uint32_t rw = r[w];  // (a bit cast of the element itself reads element 0)
-      s[w] = __builtin_bit_cast(s16x2, rw);
-    }
-    const s16x2 vmax = __builtin_elementwise_max(__builtin_elementwise_max(s[0], s[1]), __builtin_elementwise_max(s[2], s[3]));
-    const s16x2 vmin = __builtin_elementwise_min(__builtin_elementwise_min(s[0], s[1]), __builtin_elementwise_min(s[2], s[3]));
-    const s16x2 pn = __builtin_elementwise_max(pmax, vmax), nn = __builtin_elementwise_min(nmin, vmin);
-    if (pn.x != pmax.x) px = (int)v0;
-    if (pn.y != pmax.y) py = (int)v0;
-    if (nn.x != nmin.x) nx = (int)v0;
-    if (nn.y != nmin.y) ny = (int)v0;
-    pmax = pn;
-    nmin = nn;
-  });
-  // The thread's candidate as one ordered key: 0x10000 + bits for a
-  // non-negative logit, -i16(bits) for a negative one (-inf included), -1 for
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t rw = r[w];  // (a bit cast of the element itself reads element 0)
+        s[w] = __builtin_bit_cast(s16x2, rw);
+      }
+      const s16x2 vmax = __builtin_elementwise_max(__builtin_elementwise_max(s[0], s[1]), __builtin_elementwise_max(s[2], s[3]));
+      const s16x2 vmin = __builtin_elementwise_min(__builtin_elementwise_min(s[0], s[1]), __builtin_elementwise_min(s[2], s[3]));
+      const s16x2 pn = __builtin_elementwise_max(pmax, vmax), nn = __builtin_elementwise_min(nmin, vmin);
+      if (pn.x != pmax.x) px = (int)v0;
+      if (pn.y != pmax.y) py = (int)v0;
+      if (nn.x != nmin.x) nx = (int)v0;
+      if (nn.y != nmin.y) ny = (int)v0;
+      pmax = pn;
+      nmin = nn;
+    });
+    hm = pmax.x >= pmax.y ? (int)pmax.x : (int)pmax.y;
+    hp = pmax.x >= pmax.y ? px : py;
+    hn = nmin.x <= nmin.y ? (int)nmin.x : (int)nmin.y;
+    hq = nmin.x <= nmin.y ? nx : ny;
+  }
+  // The thread's candidate as one ordered key: 2^32 + bits for a
+  // non-negative logit, -int(bits) for a negative one (-inf included), -1 for
   // none.
-  int key = -1, kp = -1;
-  {
-    const int hm = pmax.x >= pmax.y ? (int)pmax.x : (int)pmax.y;
-    const int hp = pmax.x >= pmax.y ? px : py;
-    const int hn = nmin.x <= nmin.y ? (int)nmin.x : (int)nmin.y;
-    const int hq = nmin.x <= nmin.y ? nx : ny;
-    if (hm >= 0 && hm <= IO::kInf) {
-      key = 0x10000 + hm;
-      kp = hp;
-    } else if (hn <= IO::kNegInf) {
-      key = -hn;
-      kp = hq;
-    }
+  int64_t key = -1;
+  int kp = -1;
+  if (hm >= 0 && hm <= IO::kInf) {
+    key = (1ll << 32) + hm;
+    kp = hp;
+  } else if (hn <= IO::kNegInf) {
+    key = -(int64_t)hn;
+    kp = hq;
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
-    const int ok = __shfl_xor(key, o), op = __shfl_xor(kp, o);
+    const int64_t ok = __shfl_xor(key, o);
+    const int op = __shfl_xor(kp, o);
     if (ok > key || (ok == key && op < kp)) {
       key = ok;
       kp = op;
@@ -1689,7 +1726,8 @@ __global__ void __launch_bounds__(kTempThreads) __attribute__((amdgpu_waves_per_
   double best = -__builtin_huge_val();
   int bi = -1;
   if (tid == 0) {
-    int gk = red_k[0], gp = red_p[0];
+    int64_t gk = red_k[0];
+    int gp = red_p[0];
     for (int w = 1; w < kWv; ++w)
       if (red_k[w] > gk || (red_k[w] == gk && red_p[w] < gp)) {
         gk = red_k[w];
@@ -1698,9 +1736,17 @@ __global__ void __launch_bounds__(kTempThreads) __attribute__((amdgpu_waves_per_
     float lb0 = kNegInfF;
     int e = -1;  // an entry of vector gp with those bits
     if (gk >= 0 && gp >= 0) {
-      const uint32_t bits = gk >= 0x10000 ? (uint32_t)(gk - 0x10000) : ((uint32_t)(-gk) & 0xFFFFu);
-      for (int q = 0; q < NV && e < 0; ++q)
-        if (gp + q < V && (uint32_t)__builtin_bit_cast(uint16_t, x[gp + q]) == bits) e = q;
+      uint32_t bits = gk >= (1ll << 32) ? (uint32_t)(gk - (1ll << 32)) : (uint32_t)(-gk);
+      if constexpr (!k32) bits &= 0xFFFFu;
+      for (int q = 0; q < NV && e < 0; ++q) {
+        if (gp + q >= V) break;
+        uint32_t b;
+        if constexpr (k32)
+          b = __builtin_bit_cast(uint32_t, x[gp + q]);
+        else
+          b = (uint32_t)__builtin_bit_cast(uint16_t, x[gp + q]);
+        if (b == bits) e = q;
+      }
     }
     if (e >= 0) {
       // Its exact z.
@@ -1719,8 +1765,8 @@ __global__ void __launch_bounds__(kTempThreads) __attribute__((amdgpu_waves_per_
 
   // ---- pass 2: the groups that can reach the bound, queued and drawn ---------------
   float lb = lb0_s, lbl = kNegInfF;
-  // The screen (uniform over the wave): tneg and the packed operand tpk,
-  // u16(xt) + 1 or i16(xt) - 1 in both halves, for the lb of lb_t.
+  // The screen (uniform over the wave): tneg and the operand tpk, uint(xt) + 1
+  // or int(xt) - 1 (16-bit: in both halves), for the lb of lb_t.
   int tneg = 1;
   uint32_t tpk = 0;
   float lb_t = kNegInfF;
@@ -1728,12 +1774,13 @@ __global__ void __launch_bounds__(kTempThreads) __attribute__((amdgpu_waves_per_
     // At most lb - kGumbelMax: the two roundings are within 2^-23 |lb|.
     const float thr = (lb > kNegInfF && lb < -kNegInfF) ? (lb - kGumbelMax) - fabsf(lb) * 0x1p-21f : lb;
     const uint32_t xb = x_threshold_bits<LT>(thr, wp);
-    const bool neg = (xb & 0x8000u) != 0u;
-    const uint32_t c = (neg ? xb + 1u : xb - 1u) & 0xFFFFu;
+    const bool neg = (xb & (k32 ? 0x80000000u : 0x8000u)) != 0u;
+    const uint32_t c = neg ? xb + 1u : xb - 1u;
     tneg = __builtin_amdgcn_readfirstlane(neg ? 1 : 0);
-    tpk = __builtin_amdgcn_readfirstlane(c | (c << 16));
+    tpk = __builtin_amdgcn_readfirstlane(k32 ? c : ((c & 0xFFFFu) | (c << 16)));
     lb_t = lb;
   };
+  // 16-bit logits: a group is two words.
   auto screen = [&](uint32_t w0, uint32_t w1) -> bool {
     if (tneg) {
       const u16x2 m = __builtin_elementwise_min(__builtin_bit_cast(u16x2, w0), __builtin_bit_cast(u16x2, w1));
@@ -1769,17 +1816,24 @@ __global__ void __launch_bounds__(kTempThreads) __attribute__((amdgpu_waves_per_
     }
   };
   uint4* qw = qbuf[wv];
+  uint32_t* qi = qidx[wv];
   uint32_t qn = 0;  // queued groups (the same in every lane)
   auto drain = [&](uint32_t n) {  // groups [0, n), one per lane
     for (uint32_t s0 = 0; s0 < n; s0 += 64) {
       bool upd = false;
       if (s0 + (uint32_t)lane < n) {
         const uint4 it = qw[s0 + lane];
-        const float x4[4] = {raw_to_f<LT>(__builtin_bit_cast(LT, (uint16_t)(it.y & 0xFFFFu))),
-                             raw_to_f<LT>(__builtin_bit_cast(LT, (uint16_t)(it.y >> 16))),
-                             raw_to_f<LT>(__builtin_bit_cast(LT, (uint16_t)(it.z & 0xFFFFu))),
-                             raw_to_f<LT>(__builtin_bit_cast(LT, (uint16_t)(it.z >> 16)))};
-        group((int64_t)it.x, x4, upd);
+        if constexpr (k32) {
+          const float x4[4] = {__uint_as_float(it.x), __uint_as_float(it.y), __uint_as_float(it.z),
+                               __uint_as_float(it.w)};
+          group((int64_t)qi[s0 + lane], x4, upd);
+        } else {
+          const float x4[4] = {raw_to_f<LT>(__builtin_bit_cast(LT, (uint16_t)(it.y & 0xFFFFu))),
+                               raw_to_f<LT>(__builtin_bit_cast(LT, (uint16_t)(it.y >> 16))),
+                               raw_to_f<LT>(__builtin_bit_cast(LT, (uint16_t)(it.z & 0xFFFFu))),
+                               raw_to_f<LT>(__builtin_bit_cast(LT, (uint16_t)(it.z >> 16)))};
+          group((int64_t)it.x, x4, upd);
+        }
       }
       if (__ballot(upd) != 0ull) {
         float wl = lbl;
@@ -1791,15 +1845,30 @@ __global__ void __launch_bounds__(kTempThreads) __attribute__((amdgpu_waves_per_
   };
   set_threshold();
   row_sweep_words<LT, kTempThreads>(x, lo, hi, [&](int64_t v0, const u32x4& r) {
-#pragma unroll
-    for (int gq = 0; gq < NV / 4; ++gq) {
-      const uint32_t w0 = r[2 * gq], w1 = r[2 * gq + 1];
-      const bool pass = screen(w0, w1);
+    if constexpr (k32) {
+      const uint32_t a0 = r[0], a1 = r[1], a2 = r[2], a3 = r[3];
+      const bool pass = tneg ? min(min(a0, a1), min(a2, a3)) < tpk
+                             : max(max((int)a0, (int)a1), max((int)a2, (int)a3)) > (int)tpk;
       const uint64_t bal = __ballot(pass);
       if (bal != 0ull) {
-        if (pass)
-          qw[qn + (uint32_t)__popcll(bal & ((1ull << lane) - 1ull))] = make_uint4((uint32_t)(v0 + 4 * gq), w0, w1, 0u);
+        if (pass) {
+          const uint32_t q = qn + (uint32_t)__popcll(bal & ((1ull << lane) - 1ull));
+          qw[q] = make_uint4(a0, a1, a2, a3);
+          qi[q] = (uint32_t)v0;
+        }
         qn += (uint32_t)__popcll(bal);
+      }
+    } else {
+#pragma unroll
+      for (int gq = 0; gq < kGV; ++gq) {
+        const uint32_t w0 = r[2 * gq], w1 = r[2 * gq + 1];
+        const bool pass = screen(w0, w1);
+        const uint64_t bal = __ballot(pass);
+        if (bal != 0ull) {
+          if (pass)
+            qw[qn + (uint32_t)__popcll(bal & ((1ull << lane) - 1ull))] = make_uint4((uint32_t)(v0 + 4 * gq), w0, w1, 0u);
+          qn += (uint32_t)__popcll(bal);
+        }
       }
     }
     if (qn >= 64u) {
@@ -1807,8 +1876,15 @@ __global__ void __launch_bounds__(kTempThreads) __attribute__((amdgpu_waves_per_
       drain(full);
       // The rest (fewer than 64, at positions 64 and above) to the front.
       uint4 it = make_uint4(0u, 0u, 0u, 0u);
-      if ((uint32_t)lane < rest) it = qw[full + lane];
-      if ((uint32_t)lane < rest) qw[lane] = it;
+      uint32_t ix = 0;
+      if ((uint32_t)lane < rest) {
+        it = qw[full + lane];
+        if constexpr (k32) ix = qi[full + lane];
+      }
+      if ((uint32_t)lane < rest) {
+        qw[lane] = it;
+        if constexpr (k32) qi[lane] = ix;
+      }
       qn = rest;
       if (lb > lb_t + 4.f) set_threshold();
     }
@@ -1842,15 +1918,16 @@ hipError_t launch_sample_t(const AcceptArgs& a, hipStream_t s) {
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  if constexpr (sizeof(LT) == 2) {
-    if (a.sel == nullptr) {  // temperature alone
-      // One workgroup per row when the rows fill the CUs twice, else up to 8
-      // per row, each on a run of the row's ranges (each one's pass 1 reads
-      // the whole row).
-      const int64_t cus = a.cus > 0 ? a.cus : 256;
-      int64_t wpr = 2 * cus / (int64_t)rows;
-      wpr = wpr < 1 ? 1 : (wpr > 8 ? 8 : wpr);
-      wpr = wpr > a.nchunk ? a.nchunk : wpr;
+  if (a.sel == nullptr) {  // temperature alone
+    // One workgroup per row when the rows fill the CUs twice, else up to 8
+    // per row, each on a run of the row's ranges (each one's pass 1 reads the
+    // whole row).  f32 rows are twice the bytes: with fewer rows than CUs the
+    // sweep kernel draws them.
+    const int64_t cus = a.cus > 0 ? a.cus : 256;
+    int64_t wpr = 2 * cus / (int64_t)rows;
+    wpr = wpr < 1 ? 1 : (wpr > 8 ? 8 : wpr);
+    wpr = wpr > a.nchunk ? a.nchunk : wpr;
+    if (sizeof(LT) == 2 || (int64_t)rows >= cus) {
       const int64_t G = (a.nchunk + wpr - 1) / wpr;
       hipLaunchKernelGGL(sample_temp_kernel<LT>, dim3(rows, (unsigned)((a.nchunk + G - 1) / G)), dim3(kTempThreads), 0,
                          s, a);

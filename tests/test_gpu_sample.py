@@ -102,10 +102,10 @@ def test_sample_random_configurations(gpu):
         run_and_compare(lg, a.draft, a.parent_ref, a.pos, 8, temperature, top_p, top_k, seed)
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_sample_ties_at_the_top_p_cut(gpu, dtype):
-    """16-bit rows of a few repeated values, so the top-p cut falls inside a
-    tie group (kept: its highest indices) and top-k ties are all kept; with
+    """Rows of a few repeated values, so the top-p cut falls inside a tie
+    group (kept: its highest indices) and top-k ties are all kept; with
     rows whose largest logit is -0 or negative, rows of -inf and NaNs of both
     signs, also drawn with temperature alone."""
     M, V = 8, 4099
@@ -117,7 +117,10 @@ def test_sample_ties_at_the_top_p_cut(gpu, dtype):
     lg[0, 3, 17] = 2.0                              # one finite logit
     lg[0, 4, :] = float("-inf")                     # none: token 0
     lg[0, 5, 100:200] = float("nan")                # NaN counts as -inf
-    snan = torch.tensor([0x7F81, -0x7F], dtype=torch.int16).view(dtype)  # signalling NaNs, both signs
+    if dtype == torch.float32:                      # signalling NaNs, both signs
+        snan = torch.tensor([0x7F800001, -0x7FFFFF], dtype=torch.int32).view(dtype)
+    else:
+        snan = torch.tensor([0x7F81, -0x7F], dtype=torch.int16).view(dtype)
     lg[0, 6, 10], lg[0, 6, 4000] = snan[0], snan[1]
     draft = torch.randint(0, V, (1, M), generator=g)
     parent_ref = torch.tensor([[-1, 0, 1, 2, 3, 4, 5]])
@@ -132,7 +135,7 @@ def test_sample_ties_at_the_top_p_cut(gpu, dtype):
     assert r["next"][0, 3].item() == 17 and r["next"][0, 4].item() == 0
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_sample_tiny_and_huge_logits(gpu, dtype):
     """Rows of subnormal-range logits (the warper's product and quotient among
     the subnormals), rows of logits in the thousands (the fp32 bound on L
@@ -141,19 +144,20 @@ def test_sample_tiny_and_huge_logits(gpu, dtype):
     M, V = 6, 8195
     g = torch.Generator().manual_seed(12)
     base = torch.randn((1, M, V), generator=g)
-    tiny = 1e-39 if dtype == torch.bfloat16 else 1e-6  # subnormal in the dtype
+    tiny = {torch.bfloat16: 1e-39, torch.float16: 1e-6, torch.float32: 1e-41}[dtype]  # subnormal in the dtype
     lg = base.clone()
     lg[0, 0] *= tiny
     lg[0, 1] *= tiny
     lg[0, 1, 77] = 3.0
-    lg[0, 2] *= 2000.0 if dtype == torch.bfloat16 else 300.0
-    lg[0, 3] = lg[0, 3] * 2.0 + (4000.0 if dtype == torch.bfloat16 else 500.0)
+    lg[0, 2] *= 300.0 if dtype == torch.float16 else 2000.0
+    lg[0, 3] = lg[0, 3] * 2.0 + (500.0 if dtype == torch.float16 else 4000.0)
     lg[0, 4] *= 40.0
     lg = lg.to(dtype)
     draft = torch.randint(0, V, (1, M), generator=g)
     parent_ref = torch.tensor([[-1, 0, 1, 2, 3]])
     pos = torch.arange(M)
-    for temperature, top_p, top_k in [(0.3, 1.0, 5), (0.7, 0.9, 0), (1.0, 0.5, 0), (1.3, 1.0, 40), (0.7, 0.95, 20)]:
+    for temperature, top_p, top_k in [(0.3, 1.0, 5), (0.7, 0.9, 0), (1.0, 0.5, 0), (1.3, 1.0, 40), (0.7, 0.95, 20),
+                                      (0.7, 1.0, 0), (1.0, 1.0, 0)]:
         print(f"[sample tiny/huge] {dtype} T={temperature} top_p={top_p} top_k={top_k}", flush=True)
         run_and_compare(lg.to(gpu), draft.to(gpu), parent_ref.to(gpu), pos.to(gpu), 8, temperature, top_p, top_k,
                         seed=41)
