@@ -52,6 +52,26 @@ def test_sample_full_vocab_64_nodes(gpu):
     run_and_compare(a.logits, a.draft, a.parent_ref, a.pos, 8, 1.0, 1.0, 0, seed=7)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("T,V", [(1, 32768), (8, 20003)])
+def test_sample_temperature_alone_rows_and_workgroups(gpu, dtype, T, V):
+    """Temperature alone at 64 rows (16-bit logits: several workgroups per
+    row, each over a run of the row's vocabulary ranges; f32: the sweep
+    kernel) and at 512 rows (one workgroup per row, f32 included), on peaked,
+    flat, all-negative and NaN-holding rows: bit-exact against the oracle."""
+    M = 64
+    g = torch.Generator().manual_seed(17 + T)
+    lg = torch.randn((T, M, V), generator=g) * 3.0
+    lg[:, ::4, 123] += 30.0                         # a planted favourite on a quarter of the rows
+    lg[:, 1::8] -= 60.0                             # all-negative rows
+    lg[:, 2::16, 500:520] = float("nan")
+    lg = lg.to(dtype).to(gpu)
+    a = wl.make_accept_inputs(T=T, M=M, V=V, device=str(gpu), seed=5)
+    for temperature in (0.7, 1.0):
+        print(f"[sample temperature alone] {dtype} T={T} V={V} temperature={temperature}", flush=True)
+        run_and_compare(lg, a.draft, a.parent_ref, a.pos, 8, temperature, 1.0, 0, seed=1000 + T)
+
+
 def test_sample_many_rows(gpu):
     """8 trees x 64 nodes = 512 rows, at least two per CU: the select kernel
     runs its 512-thread workgroups (fewer rows take 1024 threads)."""
