@@ -1058,16 +1058,26 @@ __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) sa
       while (npad < n) npad <<= 1;
       for (int q = n + tid; q < npad; q += NT) cand[q] = 0ull;
       __syncthreads();
+      // Each stage's npad / 2 pairs (q, q | j2), q with bit j2 clear: a
+      // thread loads two pairs before comparing (the pairs of a stage are
+      // disjoint), so that their LDS round trips overlap.
       for (int k2 = 2; k2 <= npad; k2 <<= 1)
         for (int j2 = k2 >> 1; j2 > 0; j2 >>= 1) {
-          for (int q = tid; q < npad; q += NT) {
-            const int l = q ^ j2;
-            if (l > q) {
-              const uint64_t u = cand[q], w = cand[l];
-              if (((q & k2) == 0) ? (u < w) : (u > w)) {
-                cand[q] = w;
-                cand[l] = u;
-              }
+          const int lj = __builtin_ctz(j2);
+          for (int p0 = tid; p0 < npad / 2; p0 += 2 * NT) {
+            const bool h1 = p0 + NT < npad / 2;
+            const int p1 = h1 ? p0 + NT : p0;  // (without a second pair: the first again, not stored)
+            const int q0 = ((p0 >> lj) << (lj + 1)) | (p0 & (j2 - 1));
+            const int q1 = ((p1 >> lj) << (lj + 1)) | (p1 & (j2 - 1));
+            const uint64_t u0 = cand[q0], w0 = cand[q0 | j2];
+            const uint64_t u1 = cand[q1], w1 = cand[q1 | j2];
+            if (((q0 & k2) == 0) ? (u0 < w0) : (u0 > w0)) {
+              cand[q0] = w0;
+              cand[q0 | j2] = u0;
+            }
+            if (h1 && (((q1 & k2) == 0) ? (u1 < w1) : (u1 > w1))) {
+              cand[q1] = w1;
+              cand[q1 | j2] = u1;
             }
           }
           __syncthreads();
