@@ -289,8 +289,9 @@ int dsv_tree_accept(int mode, const dsv_tensor* logits, const dsv_tensor* draft,
  * operations, so the draws are reproducible bit for bit; they are samples of
  * softmax(y) over the kept set.  A row without a finite logit draws token 0.
  *   logits, draft, parent, pos, max_hops, out_*: as dsv_tree_accept;
- *   out_next receives the per-node draws.  temperature >= 1e-5 (the
- *   reference takes the greedy branch below it).  Workspace:
+ *   out_next receives the per-node draws.  temperature > 1e-5, compared in
+ *   double precision (the reference takes the greedy branch at or below
+ *   it).  Workspace:
  *   dsv_accept_workspace_bytes.
  */
 int dsv_tree_accept_sample(const dsv_tensor* logits, const dsv_tensor* draft,

@@ -1239,8 +1239,11 @@ int dsv_tree_accept_sample(const dsv_tensor* logits, const dsv_tensor* draft, co
   if (logits->dtype != DSV_BF16 && logits->dtype != DSV_F16 && logits->dtype != DSV_F32)
     return fail(DSV_ERR_INVALID, "logits must be bf16, f16 or f32");
   if (logits->stride[2] != 1) return fail(DSV_ERR_INVALID, "logits vocab stride must be 1");
-  if (!(temperature >= 1e-5f) || !(temperature < __builtin_huge_valf()))
-    return fail(DSV_ERR_INVALID, "temperature must be >= 1e-5 (smaller temperatures are greedy acceptance)");
+  // The reference builds its warpers only when temperature > 1e-5 (compared in
+  // double precision, draft/tree_verification.py:21); at or below it the
+  // walk is greedy (dsv_tree_accept).
+  if (!((double)temperature > 1e-5) || !(temperature < __builtin_huge_valf()))
+    return fail(DSV_ERR_INVALID, "temperature must be > 1e-5 (smaller temperatures are greedy acceptance)");
   if (!(top_p >= 0.f && top_p <= 1.f)) return fail(DSV_ERR_INVALID, "top_p must lie in [0, 1]");
   if (top_k < 0) return fail(DSV_ERR_INVALID, "top_k must be >= 0");
   const int64_t T = logits->shape[0], M = logits->shape[1], V = logits->shape[2];

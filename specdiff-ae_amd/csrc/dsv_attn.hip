@@ -309,10 +309,13 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
     const int64_t wb = wg_base_elem(src, dma_v, b, kvh);
     rs = make_rsrc((dma_v ? src.v : src.k) + wb, rsrc_range(dma_v ? src.v_bytes : src.k_bytes, wb));
   }
-  // Page window (32-bit paged mode): lane l of pgw[x] holds the physical page
-  // of this wave's DMA instruction x in full tile pgw_t0 + l, so that a tile's
-  // page costs a lane read instead of an LDS round trip; the window is
-  // refilled from the LDS page-table slice once per 64 tiles.
+  // Page window (32-bit paged mode): lane l of pgw[x] holds the byte offset,
+  // from the workgroup's buffer base, of this wave's DMA instruction x in full
+  // tile pgw_t0 + l (physical page * page stride + key-in-page * key stride),
+  // so that a tile's address costs one lane read instead of an LDS round trip
+  // and its scalar arithmetic.  The window is refilled from the LDS page-table
+  // slice once per 64 tiles; windows start at tile 0 and every 64th tile, all
+  // multiples of 4, so only ring stage 0 can start one.
   uint32_t pgw[IPW];
   int pgw_t0 = -64;
 #pragma unroll
@@ -327,7 +330,8 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
       dma_ins<D>(wid * IPW + x, is_v, j);
       const uint32_t nb = (uint32_t)(src.key0 + kstart) + (uint32_t)(t0 + lane) * KT + (uint32_t)(j * G::KPI);
       const int e = min((int)(nb >> src.ps_shift) - (int)pt_lo, last);  // lanes past the split: any valid entry
-      pgw[x] = (uint32_t)pt_lds[e];
+      pgw[x] = tile_off32_s(true, (uint32_t)(2 * (is_v ? src.v_st : src.k_st)), (uint32_t)(2 * (is_v ? src.v_sp : src.k_sp)),
+                            (1u << src.ps_shift) - 1u, nb, (uint32_t)pt_lds[e]);
     }
   };
 
@@ -342,9 +346,9 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
   auto issue_tile = [&](auto stage_c, int t) {
     constexpr int stage = decltype(stage_c)::value;
     if (MODE != kModeAny && t < nfull) {
-      // Full tile in a 32-bit mode: scalar key arithmetic, the lane offsets of
-      // voff_full, the page from the window.
-      if (MODE == kModeF32Paged && t - pgw_t0 >= 64) fill_pgw(t);
+      // Full tile in a 32-bit mode: the lane offsets of voff_full plus the
+      // tile's offset (from the window when paged).
+      if (MODE == kModeF32Paged && stage == 0 && t - pgw_t0 >= 64) fill_pgw(t);
       const uint32_t nbt = key0_32 + (uint32_t)t * KT;
 #pragma unroll
       for (int x = 0; x < IPW; ++x) {
@@ -352,9 +356,9 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
         int j;
         dma_ins<D>(wid * IPW + x, is_v, j);
         const uint32_t dst = lds_addr(smem + (stage * 2 + (is_v ? 1 : 0)) * G::TILE + j * 1024);
-        const uint32_t page =
-            MODE == kModeF32Paged ? (uint32_t)__builtin_amdgcn_readlane((int)pgw[x], t - pgw_t0) : 0u;
-        dma_rs(dst, rs, voff_full[x] + tile_off32_s(MODE == kModeF32Paged, st2, sp2, psm, nbt + (uint32_t)(j * G::KPI), page));
+        const uint32_t toff = MODE == kModeF32Paged ? (uint32_t)__builtin_amdgcn_readlane((int)pgw[x], t - pgw_t0)
+                                                    : tile_off32_s(false, st2, sp2, psm, nbt + (uint32_t)(j * G::KPI), 0u);
+        dma_rs(dst, rs, voff_full[x] + toff);
       }
       return;
     }
@@ -688,14 +692,25 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
       *reinterpret_cast<u32x2*>(stage + lj * (2 * D) + ((c ^ (lj % CHR)) * 16) + 8 * lg) = val;
     }
   }
+  // Each lane now reads 16-byte chunks that other lanes of this wave wrote:
+  // order the reads after the writes explicitly (wave-scope release, wave
+  // barrier, acquire), so no compiler reordering can move them ahead.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   const int64_t pbase = (((int64_t)split * a.B + b) * a.Hk + kvh) * a.R + row0;
   uint16_t* op = a.opart + pbase * D;
+  // All of the lane's chunks are read from LDS first (one wait), then stored.
+  u32x4 chunk[CHR / 2];
 #pragma unroll
   for (int k = 0; k < CHR / 2; ++k) {
     const int f = k * 64 + lane, r = f / CHR, i = f % CHR;
-    if (row0 + r < a.R)
-      *reinterpret_cast<u32x4*>(op + (int64_t)r * D + i * 8) =
-          *reinterpret_cast<const u32x4*>(stage + r * (2 * D) + ((i ^ (r % CHR)) * 16));
+    chunk[k] = *reinterpret_cast<const u32x4*>(stage + r * (2 * D) + ((i ^ (r % CHR)) * 16));
+  }
+#pragma unroll
+  for (int k = 0; k < CHR / 2; ++k) {
+    const int f = k * 64 + lane, r = f / CHR, i = f % CHR;
+    if (row0 + r < a.R) *reinterpret_cast<u32x4*>(op + (int64_t)r * D + i * 8) = chunk[k];
   }
   if (rvalid && lg == 0) a.ml[pbase + lj] = make_float2(mx, ltot);
 }

@@ -1122,8 +1122,10 @@ __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) sa
       const double Lq = (double)L * __builtin_ldexp(1.0, S);
       const double eps = ((double)((V + NT - 1) / NT) + 8.0 + kWaves) * 0x1p-24 + 0x1p-16 +
                          0x1p-22 * __builtin_fabs((double)m);
+      // Every mass is at most 2^S and V * 2^S < 2^63, so L < 2^63: the upper
+      // bound is capped there (and still converts to uint64 exactly).
       const double llo = __builtin_fmax(0.0, Lq * (1.0 - eps) - (double)V);
-      const double lhi = __builtin_fmin(Lq * (1.0 + eps) + (double)V + 1.0, 0x1p62);
+      const double lhi = __builtin_fmin(Lq * (1.0 + eps) + (double)V + 1.0, 0x1p63);
       const uint64_t L_lo = max(H, (uint64_t)__builtin_floor(llo));
       const uint64_t L_hi = max(H, (uint64_t)__builtin_ceil(lhi));
       const uint64_t tq_lo = tq_of(a.top_p_q, L_lo);
@@ -1150,7 +1152,7 @@ __global__ void __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) sa
       __syncthreads();
       // Decided: the first non-candidate (mass H above it) is dropped for
       // every L in the bounds, and so is the same head of the candidates.
-      ok = H >= tq_hi && nk_lo == nk_hi;
+      ok = L_lo <= L_hi && H >= tq_hi && nk_lo == nk_hi;
       nkeep = (int)nk_hi;
     }
     if (ok) {

@@ -28,6 +28,12 @@ def sdpa_backend_name() -> str:
     return "dsv_hip_gfx950"
 
 
+def _slice_len(n: int, N: int) -> int:
+    """Keys kept by the reference's ``k_cache[:, :n]`` (attention_compat.py:113):
+    Python slicing, so n > N keeps all N and a negative n drops -n from the end."""
+    return len(range(N)[:n])
+
+
 def flash_attn_func(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, dropout_p: float = 0.0,
                     causal: bool = False, window_size=None, **_: object) -> torch.Tensor:
     if dropout_p:
@@ -44,7 +50,7 @@ def flash_attn_with_kvcache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
     seqlens, n = None, N
     if isinstance(cache_seqlens, torch.Tensor):
         if cache_seqlens.numel() == 1 and cache_seqlens.dim() == 0:
-            n = min(int(cache_seqlens.item()), N)
+            n = _slice_len(int(cache_seqlens.item()), N)
         else:
             seqlens = cache_seqlens.reshape(-1)
             if seqlens.numel() != B:
@@ -53,7 +59,7 @@ def flash_attn_with_kvcache(q: torch.Tensor, k_cache: torch.Tensor, v_cache: tor
                 seqlens = seqlens.to(torch.int64)
             seqlens = seqlens.to(dev).contiguous()
     elif cache_seqlens is not None:
-        n = int(cache_seqlens)
+        n = _slice_len(int(cache_seqlens), N)
     lib = _ext.load()
     out = torch.empty_like(q)
     lse = torch.empty((B, H, M), dtype=torch.float32, device=dev) if return_softmax_lse else None

@@ -11,6 +11,7 @@ import ctypes
 import re
 from pathlib import Path
 
+import numpy as np
 import pytest
 import torch
 
@@ -157,6 +158,13 @@ def test_accept_sample_validation(dsv_lib):
 
     assert call(temperature=0.0) == -1 and "temperature" in _ext.last_error()
     assert call(temperature=float("nan")) == -1 and "temperature" in _ext.last_error()
+    # The reference samples only when temperature > 1e-5 (in double precision):
+    # the float nearest 1e-5 lies below it and is refused; the next one up
+    # passes the check (and fails later, on the fake workspace).
+    f_1e5 = float(np.float32(1e-5))
+    assert f_1e5 < 1e-5 and call(temperature=f_1e5) == -1 and "temperature" in _ext.last_error()
+    above = float(np.nextafter(np.float32(1e-5), np.float32(1.0)))
+    assert above > 1e-5 and call(temperature=above) == -3 and "workspace" in _ext.last_error()
     assert call(top_p=1.5) == -1 and "top_p" in _ext.last_error()
     assert call(top_p=-0.1) == -1 and "top_p" in _ext.last_error()
     assert call(top_k=-1) == -1 and "top_k" in _ext.last_error()

@@ -84,6 +84,15 @@ def test_prefix_attention_expanded_kv_and_cache_seqlens(gpu):
     o_ref, l_ref = oa.prefix_attention(np64(q[0]), np64(k2[0, :123]), np64(v2[0, :123]))
     assert_attn_close(np64(o3[0]), o_ref)
     assert_lse_close(np64(l3[0]), l_ref)
+    # A scalar length is the reference's k_cache[:, :n] (attention_compat.py:113):
+    # an int or 0-dim tensor beyond N keeps all N keys, a negative one drops -n
+    # keys from the end, in both forms alike.
+    for n, keys in [(N + 50, N), (-20, N - 20)]:
+        for cs in (n, torch.tensor(n)):
+            o4, l4 = flash_attn_with_kvcache(q, k2, v2, cache_seqlens=cs, return_softmax_lse=True)
+            o_ref, l_ref = oa.prefix_attention(np64(q[0]), np64(k2[0, :keys]), np64(v2[0, :keys]))
+            assert_attn_close(np64(o4[0]), o_ref, what=f"cache_seqlens={cs!r}")
+            assert_lse_close(np64(l4[0]), l_ref, what=f"cache_seqlens={cs!r}")
 
 
 @pytest.mark.parametrize("causal", [False, True])

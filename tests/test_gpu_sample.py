@@ -209,6 +209,35 @@ def test_sample_rows_with_infinite_logits(gpu, dtype):
                         seed=31)
 
 
+def test_sample_top_p_total_mass_above_2_62(gpu):
+    """Rows whose fixed-point total mass L lies just above 2^62 (V = 8000, so
+    S = 50 and L < 2^63): four logits tied at the maximum and a flat tail that
+    brings L to 4096.01 * 2^50, with top_p = 2^-12, so that the exact cut
+    P * L / 2^32 lies just above one tie's mass and keeps two of the four
+    tied entries (the two highest indices).  An upper bound of L capped at
+    2^62 would keep one.  The sixteen nodes draw between the two kept entries;
+    every draw is checked against the oracle."""
+    V, M, h = 8000, 16, 4
+    a = np.float32(-0.66990507)
+    row = np.full(V, a, dtype=np.float32)
+    row[:h] = 0.0
+    q = sp.fixed_masses(row.astype(np.float64))
+    L = int(q.sum(dtype=np.uint64))
+    assert 2 ** 62 < L < 2 ** 62 + 2 ** 50 // 10
+    top_p = 2.0 ** -12
+    assert sp.kept_mask(row.astype(np.float64), top_p, 0).sum() == 2
+    for shift in (0, 3001):                         # the tied entries at the front, then mid-row
+        lg = torch.from_numpy(np.roll(row, shift)).reshape(1, 1, V).repeat(1, M, 1)
+        g = torch.Generator().manual_seed(shift)
+        draft = torch.randint(0, V, (1, M), generator=g)
+        parent_ref = torch.tensor([list(range(-1, M - 2))])
+        pos = torch.arange(M)
+        print(f"[sample L>2^62] shift {shift}", flush=True)
+        r = run_and_compare(lg.to(gpu), draft.to(gpu), parent_ref.to(gpu), pos.to(gpu), 8, 1.0, top_p, 0, seed=17)
+        draws = set(r["next"][0].cpu().tolist())
+        assert draws == {shift + 2, shift + 3}, draws
+
+
 @pytest.mark.parametrize("temperature,top_p,top_k", [(1.0, 1.0, 0), (0.6, 0.85, 0), (1.5, 1.0, 6)])
 def test_sample_frequencies_follow_the_warped_softmax(gpu, temperature, top_p, top_k):
     """4096 draws of one 24-token row (512 trees x 8 nodes with the same logits)."""
