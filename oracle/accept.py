@@ -7,8 +7,10 @@ Test infrastructure only (see oracle/__init__.py).
 torch.argmax does).  ``typical_walk`` applies the posterior criterion of
 Cai et al. 2024 (Medusa): accept node i iff
     p_T(draft[i] | parent) > min(eps, alpha * exp(-H(p_T(. | parent))))
-with p_T = softmax(logits / T) and H its exact entropy (0 log 0 = 0); the
-reference has no typical mode, so this function defines it.
+with p_T = softmax(logits / T) and H its exact entropy (0 log 0 = 0),
+evaluated in float64; T, eps and alpha are taken as the float32 values the
+C ABI receives.  The reference has no typical mode, so this function defines
+it.
 ``brute_force_greedy`` is an independent formulation used to pin
 ``greedy_walk``: a node is accepted iff every edge on its root path matches.
 ``kv_commit`` restates the KV compaction after the walk
@@ -78,11 +80,22 @@ def softmax_stats(row: np.ndarray, temperature: float = 1.0) -> Tuple[np.ndarray
     return p, ent
 
 
+def f32(x: float) -> float:
+    """x rounded to float32 (the C ABI's argument type), as a Python float."""
+    return float(np.float32(x))
+
+
+def typical_prob_thr(row: np.ndarray, tok: int, temperature: float, eps: float, alpha: float) -> Tuple[float, float]:
+    """(p_T(tok), min(eps, alpha * exp(-H))) with float32-rounded T, eps, alpha."""
+    p, ent = softmax_stats(row, f32(temperature))
+    return float(p[tok]), float(min(f32(eps), f32(alpha) * np.exp(-ent)))
+
+
 def typical_accept(row: np.ndarray, tok: int, temperature: float, eps: float, alpha: float) -> bool:
-    p, ent = softmax_stats(row, temperature)
-    if tok < 0 or tok >= p.size:
+    if tok < 0 or tok >= np.asarray(row).size:
         return False
-    return bool(p[tok] > min(eps, alpha * np.exp(-ent)))
+    prob, thr = typical_prob_thr(row, tok, temperature, eps, alpha)
+    return bool(prob > thr)
 
 
 def typical_walk(logits: np.ndarray, draft: Sequence[int], parent_ref: Sequence[int], pos: Sequence[int],

@@ -502,6 +502,85 @@ __global__ void __launch_bounds__(kStrThreads) accept_stream16_kernel(const Acce
   }
 }
 
+// Relative margin around the typical threshold within which the fp32
+// decision is not trusted.  The sweep's statistics carry relative errors of
+// about 2^-16 from the fp32 sums (at most a few hundred terms per thread,
+// then tree merges) plus 2^-20 (1 + |m| + 12) from the per-element
+// exponentials and the rounded 1/T log2(e) (weighted by the probabilities,
+// whose mean distance below the maximum m is at most the entropy, <= ln V);
+// the entropy's error, through s / l, is that relative error times at most
+// |m| + 13 (natural units).  At |m| = 10 this is below 1e-3 relative in the
+// threshold; the margin 2^-7 (1 + |m| / 16) is more than ten times the bound.
+__device__ __forceinline__ float typical_margin(float m_log2) {
+  return 0x1p-7f * (1.f + fabsf(m_log2 * kLn2) * 0.0625f);
+}
+
+__device__ __forceinline__ double logit_at(const AcceptArgs& a, int64_t off) {
+  if (a.l_dtype == 0) return (double)__uint_as_float((uint32_t)reinterpret_cast<const uint16_t*>(a.logits)[off] << 16);
+  if (a.l_dtype == 1) return (double)(float)reinterpret_cast<const _Float16*>(a.logits)[off];
+  return (double)reinterpret_cast<const float*>(a.logits)[off];
+}
+
+// Block-wide reductions of a double (every thread gets the result).
+__device__ __forceinline__ double block_sum_d(double v, double* scratch) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  const int nw = (blockDim.x + 63) >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
+  __syncthreads();
+  double r = 0.0;
+  for (int w = 0; w < nw; ++w) r += scratch[w];
+  return r;
+}
+// Maximum that propagates NaN (numpy's max).
+__device__ __forceinline__ double nan_max(double x, double y) { return (x != x || y != y) ? x + y : (x > y ? x : y); }
+__device__ __forceinline__ double block_max_d(double v, double* scratch) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = nan_max(v, __shfl_xor(v, o));
+  const int nw = (blockDim.x + 63) >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
+  __syncthreads();
+  double r = scratch[0];
+  for (int w = 1; w < nw; ++w) r = nan_max(r, scratch[w]);
+  return r;
+}
+
+// The typical test of every flagged node (okv[n] == 2) decided from float64
+// statistics of its parent's row, the definition's own arithmetic:
+//   y = x / T, m = max y, z = sum e^(y - m), H = m + ln z - sum_{e > 0} e^(y - m) y / z,
+//   accept iff e^(y_tok - m) / z > min(eps, alpha e^-H)
+// with T, eps and alpha the arguments as given (float).  The whole workgroup
+// takes one flagged node at a time: two passes over the parent's row.
+__device__ __noinline__ void typical_recheck(const AcceptArgs& a, int t, const int* par, int* okv, const float* xtok) {
+  __shared__ double scratch[16];
+  const double T = (double)a.temperature;
+  const int64_t V = a.V;
+  for (int n = 1; n < a.M; ++n) {
+    if (okv[n] != 2) continue;  // uniform: every thread reads the same LDS word
+    const int64_t base = (int64_t)t * a.l_st + (int64_t)par[n] * a.l_sm;
+    double mx = -__builtin_huge_val();
+    for (int64_t v = threadIdx.x; v < V; v += blockDim.x) mx = nan_max(mx, logit_at(a, base + v) / T);
+    mx = block_max_d(mx, scratch);
+    double z = 0.0, sy = 0.0;
+    for (int64_t v = threadIdx.x; v < V; v += blockDim.x) {
+      const double y = logit_at(a, base + v) / T;
+      const double e = exp(y - mx);
+      z += e;
+      if (e > 0.0) sy += e * y;
+    }
+    z = block_sum_d(z, scratch);
+    sy = block_sum_d(sy, scratch);
+    const double ent = mx + log(z) - sy / z;
+    const double prob = exp((double)xtok[n] / T - mx) / z;
+    const double thr = fmin((double)a.eps, (double)a.alpha * exp(-ent));
+    __syncthreads();
+    if (threadIdx.x == 0) okv[n] = prob > thr;
+    __syncthreads();
+  }
+}
+
 __global__ void __launch_bounds__(1024) accept_walk_kernel(const AcceptArgs a) {
   extern __shared__ int64_t smem64[];
   const int M = a.M;
@@ -614,7 +693,12 @@ __global__ void __launch_bounds__(1024) accept_walk_kernel(const AcceptArgs a) {
   }
   __syncthreads();
 
-  // 3. Per-node acceptance test against the parent's distribution.
+  // 3. Per-node acceptance test against the parent's distribution.  The
+  // typical test is decided from the sweep's fp32 statistics unless the
+  // draft token's probability lies within the margin typical_margin() of the
+  // threshold: such nodes (okv = 2) are decided again from float64
+  // statistics of the parent's row, below.
+  bool recheck = false;
   if (i < M) {
     int ok = 1;
     if (i > 0) {
@@ -627,10 +711,18 @@ __global__ void __launch_bounds__(1024) accept_walk_kernel(const AcceptArgs a) {
           const float prob = __builtin_amdgcn_exp2f(fmaf(xtok, a.inv_temp * kLog2e, -mz[p])) / lz[p];
           const float thr = fminf(a.eps, a.alpha * __expf(-hz[p]));
           ok = prob > thr;
+          recheck = a.xtok == nullptr && a.logits != nullptr && prob == prob && thr == thr &&
+                    fabsf(prob - thr) <= typical_margin(mz[p]) * thr;
         }
       }
     }
-    okv[i] = ok;
+    okv[i] = recheck ? 2 : ok;
+  }
+  if (__syncthreads_or(recheck)) {
+    // The flagged nodes' draft-token logits (lz is not read again).
+    if (recheck) lz[i] = xtok;
+    __syncthreads();
+    typical_recheck(a, t, par, okv, lz);
   }
   __syncthreads();
 
@@ -800,6 +892,10 @@ __global__ void __launch_bounds__(kRowThreads) accept_combine_kernel(const Accep
 
 size_t accept_walk_lds_bytes(int M);
 
+// The walk runs one thread per node, and at least 256 threads so that the
+// typical re-check streams a row with a whole workgroup.
+static int walk_threads(int M) { return std::max(256, ((M + 63) / 64) * 64); }
+
 hipError_t launch_accept_from_parts(const AcceptArgs& a, const float4* part, const float* part2, int nin,
                                     hipStream_t s) {
   if (a.T <= 0 || a.M <= 0) return hipSuccess;
@@ -810,7 +906,7 @@ hipError_t launch_accept_from_parts(const AcceptArgs& a, const float4* part, con
     hipLaunchKernelGGL(accept_combine_kernel<false>, grid, dim3(kRowThreads), 0, s, a, part, part2, nin);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int threads = ((a.M + 63) / 64) * 64;
+  const int threads = walk_threads(a.M);
   hipLaunchKernelGGL(accept_walk_kernel, dim3((unsigned)a.T), dim3(threads), accept_walk_lds_bytes(a.M), s, a);
   return hipGetLastError();
 }
@@ -863,7 +959,7 @@ hipError_t launch_accept(const AcceptArgs& a, hipStream_t s, hipEvent_t ev0, hip
 }
 
 hipError_t launch_walk(const AcceptArgs& a, hipStream_t s) {
-  const int threads = ((a.M + 63) / 64) * 64;
+  const int threads = walk_threads(a.M);
   hipLaunchKernelGGL(accept_walk_kernel, dim3((unsigned)a.T), dim3(threads), accept_walk_lds_bytes(a.M), s, a);
   return hipGetLastError();
 }

@@ -1177,6 +1177,7 @@ static int accept_common(int mode, int64_t T, int64_t M, int64_t V, const dsv_te
   a.pos_sm = pos->stride[pos->ndim - 1];
   a.max_hops = (int)std::min<int64_t>(max_hops, 1 << 20);
   a.inv_temp = mode == DSV_ACCEPT_TYPICAL ? 1.f / temperature : 1.f;
+  a.temperature = mode == DSV_ACCEPT_TYPICAL ? temperature : 1.f;  // the typical re-check's T
   a.eps = posterior_threshold;
   a.alpha = posterior_alpha;
   a.out_path = static_cast<int64_t*>(out_path->data);
