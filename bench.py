@@ -12,10 +12,12 @@ bf16 + LSE [64, 32].  Four distinct KV layers are rotated so the 256 MiB
 per-layer K/V set is not served from the 256 MB Infinity Cache.
 
 Also measured (extra fields): the acceptance kernel on 8 trees x 64 nodes x
-vocab 128256 bf16 (greedy and typical), and the CPU baseline — the
-reference's own torch CPU path (repeat_kv -> fp32 matmul/softmax/logsumexp
-prefix -> naive tree -> sigmoid merge) on the same workload, timed on the
-host cores.
+vocab 128256 bf16 (greedy, typical, sampling), the 128K / 128-node
+bundle-packed verify, the 32-layer Llama-3.1-8B-shaped step, and the CPU
+baseline — the reference's own torch CPU path (repeat_kv -> fp32
+matmul/softmax/logsumexp prefix -> naive tree -> sigmoid merge) on the same
+workload, its greedy walk, and the 4096-token fp32 layer, timed on the host
+cores.
 
 Prints ONE JSON line.
 """
@@ -68,6 +70,12 @@ class HipEvents:
                 raise RuntimeError(f"hipEventCreate failed ({rc})")
             evs.append(e)
         return evs
+
+    def record(self, e, stream):
+        self.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        rc = self.hip.hipEventRecord(e, ctypes.c_void_p(stream))
+        if rc != 0:
+            raise RuntimeError(f"hipEventRecord failed ({rc})")
 
     def elapsed_ms(self, a, b):
         ms = ctypes.c_float()
@@ -282,11 +290,29 @@ def bench_llama8b_step(args, lib, ev):
     # and replayed (Python launch overhead excluded; eager launching leaves the
     # GPU idle between this scaffolding's small torch ops).
     us_step = device_us(st.step, calls=1, reps=5)
-    # Attention's device time: one layer's fused verify (kernels 1 and 3),
-    # replayed, times the 32 layers.
-    attn_one = device_us(lambda: tree_verify(inp.q, inp.kv_pages[0, 0], inp.kv_pages[0, 1], N, st.par,
-                                             page_table=inp.page_table), calls=10, reps=10)
-    attn_us = L * attn_one
+    # Attention's device time inside the step: in eager steps, each layer's
+    # fused verify (kernels 1 and 3, over that layer's own KV pages) is timed
+    # from a HIP event attached to its kernel-1 launch (the kernel's start)
+    # to an event recorded on the stream right after the call (after kernel
+    # 3).  The host enqueues kernel 3 and that event while kernel 1 runs, so
+    # the interval holds no host gap.
+    attn_steps = []
+    stream = torch.cuda.current_stream().cuda_stream
+    for _ in range(3):
+        evs = ev.create(3 * L)
+
+        def hook(l, phase):
+            if phase == 0:
+                lib.dsv_set_timing_events(evs[3 * l], evs[3 * l + 1])
+            else:
+                ev.record(evs[3 * l + 2], stream)
+
+        st.step(verify_hook=hook)
+        torch.cuda.synchronize()
+        attn_steps.append([ev.elapsed_ms(evs[3 * l], evs[3 * l + 2]) * 1e3 for l in range(L)])
+        ev.destroy(evs)
+    per_layer = [statistics.median(s_[l] for s_ in attn_steps) for l in range(L)]
+    attn_us = sum(per_layer)
     commit = bench_commit(inp, N, M, L, Hk, D, n)
     # The append alone (one layer): q/k RoPE + tree K/V into the pages, one
     # launch, against the reference's ops (RoPE of q and k in bf16 torch ops,
@@ -324,6 +350,10 @@ def bench_llama8b_step(args, lib, ev):
             "timing": "us_per_step: device time of the step, HIP graph replayed; us_per_step_eager: eager "
                       "launches (host-bound: the torch scaffolding's launches leave the GPU idle)",
             "attention_us_per_step": round(attn_us, 1), "attention_share": round(attn_us / us_step, 3),
+            "attention_us_per_layer": {"min": round(min(per_layer), 2), "median": round(statistics.median(per_layer), 2),
+                                       "max": round(max(per_layer), 2)},
+            "attention_timing": "sum over the 32 layers of each layer's fused verify inside the step (its own KV "
+                                "pages): kernel-1 start event to an event after kernel 3, median of 3 eager steps",
             "weight_bytes": wbytes, "kv_bytes": kvbytes,
             "hbm_gbs": round((wbytes + kvbytes) / (us_step * 1e-6) / 1e9, 1),
             "planted_path_len": len(path), "accept_length": alen,
@@ -399,6 +429,41 @@ def bench_commit(inp, N, M, L, Hk, D, n):
             "timing": "device time per call, HIP graph replayed"}
 
 
+def bench_fp32_4k():
+    """The 4096-token fp32 layer on the GPU: N=4096, M=64, GQA 32/8, D=128,
+    Q / K-V prefix / K-V tree drawn N(0, 1) fp32 in that order (seed 0), the
+    64-node tree; fp32 tensors straight into the fp32 kernel (kernel 1's fp32
+    variant + kernel 3).  Then the greedy walk over [1, 64, 128256] fp32
+    N(0, 3) logits (seed 1) with uniform draft tokens.  Device time per call,
+    HIP graph replayed."""
+    from diffspec_mi355x import workloads as wl
+    from diffspec_mi355x.draft.tree_verification import tree_accept
+    from diffspec_mi355x.runtime.tree_attention import tree_verify
+
+    g = torch.Generator().manual_seed(0)
+    M, H, Hk, D, N = 64, 32, 8, 128, 4096
+    q = torch.randn(1, M, H, D, generator=g)
+    kp, vp = torch.randn(1, N, Hk, D, generator=g), torch.randn(1, N, Hk, D, generator=g)
+    kt, vt = torch.randn(1, M, Hk, D, generator=g), torch.randn(1, M, Hk, D, generator=g)
+    parent, depth = wl.make_tree(M, seed=0)
+    q, kc, vc = q.cuda(), torch.cat([kp, kt], 1).cuda(), torch.cat([vp, vt], 1).cuda()
+    par = torch.tensor(parent, dtype=torch.int64, device="cuda")
+    attn = device_us(lambda: tree_verify(q, kc, vc, N, par, out_dtype=torch.float32))
+    g = torch.Generator().manual_seed(1)
+    V = 128256
+    logits = (torch.randn((1, M, V), generator=g) * 3.0).cuda()
+    draft = torch.randint(0, V, (1, M), generator=g).cuda()
+    pref = torch.tensor([wl.parent_to_reference(parent)], dtype=torch.int64, device="cuda")
+    pos = torch.tensor(depth, dtype=torch.int64, device="cuda")
+    walk = device_us(lambda: tree_accept(logits, draft, pref, pos, 10))
+    flops = 4 * M * H * (N + M) * D
+    return {"workload": "tree-verify attention, 1 layer, N=4096, M=64, fp32 dense KV; greedy walk over "
+                        "[1, 64, 128256] fp32 logits",
+            "attention_us": round(attn, 2), "greedy_walk_us": round(walk, 2), "total_us": round(attn + walk, 2),
+            "attention_tflops_fp32": round(flops / (attn * 1e-6) / 1e12, 1),
+            "timing": "device time per call, HIP graph of 10 calls replayed"}
+
+
 def bench_accept(args, lib, ev):
     from diffspec_mi355x import workloads as wl
     from diffspec_mi355x.draft.tree_verification import tree_accept
@@ -450,8 +515,25 @@ def bench_accept(args, lib, ev):
     return res
 
 
+def _cpu_median_us(fn, seconds, max_runs):
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or not times:
+        t0 = time.perf_counter()
+        out = fn()
+        times.append(time.perf_counter() - t0)
+        if len(times) >= max_runs:
+            break
+    return statistics.median(times) * 1e6, len(times), out
+
+
 def cpu_baseline(inp, args):
-    """Reference CPU path (oracle/ref_cpu_path.py) on the same layer, bounded sample."""
+    """The reference's CPU path (oracle/ref_cpu_path.py), bounded samples:
+    the verify attention of the same layer (repeat_kv -> fp32 prefix ->
+    naive tree -> sigmoid merge), the greedy walk over [1, 64, 128256] fp32
+    N(0, 3) logits (seed 1; draft/tree_verification.py:100-182), and the
+    4096-token fp32 layer (seed 0) with the same walk."""
+    from diffspec_mi355x import workloads as wl
     from oracle import ref_cpu_path as rc
     from oracle import attention as oa
 
@@ -465,18 +547,43 @@ def cpu_baseline(inp, args):
     v = inp.logical_kv(0, 1)[0].float().cpu().transpose(0, 1).unsqueeze(0).contiguous()
     q = inp.q.float().cpu()
     mask = rc.additive_tree_mask(torch.from_numpy(oa.ancestor_mask(inp.parent)))
-    times = []
-    t_end = time.perf_counter() + args.cpu_seconds
-    while time.perf_counter() < t_end or not times:
-        t0 = time.perf_counter()
-        out = rc.hybrid_verify_cpu(q, k, v, n_prefix, mask)
-        times.append(time.perf_counter() - t0)
-        if len(times) >= args.cpu_max_steps:
-            break
-    return {"value": statistics.median(times) * 1e6, "unit": "us/verify-step", "cores": cores,
+    attn_us, n_attn, out = _cpu_median_us(lambda: rc.hybrid_verify_cpu(q, k, v, n_prefix, mask), args.cpu_seconds,
+                                          args.cpu_max_steps)
+    del k, v
+
+    # The greedy walk of one step: logits [1, 64, 128256] fp32 N(0, 3), seed 1,
+    # uniform draft tokens (seed 1), the 64-node tree of the generator.
+    V = 128256
+    g = torch.Generator().manual_seed(1)
+    logits = torch.randn((1, M, V), generator=g) * 3.0
+    draft = torch.randint(0, V, (1, M), generator=g)
+    parent, depth = wl.make_tree(M, seed=0)
+    pref = torch.tensor(wl.parent_to_reference(parent), dtype=torch.int64)
+    pos = torch.tensor(depth, dtype=torch.int64)
+    walk_us, n_walk, _ = _cpu_median_us(lambda: rc.greedy_walk_torch(logits, draft, pref, pos, 8), 3.0, 20)
+
+    # The 4096-token fp32 layer: Q, K/V prefix, K/V tree drawn N(0, 1) in that
+    # order (seed 0), GQA 32/8, D 128, the same 64-node tree.
+    g = torch.Generator().manual_seed(0)
+    H, Hk, D, N1 = 32, 8, 128, 4096
+    q1 = torch.randn(1, M, H, D, generator=g)
+    kp, vp = torch.randn(1, N1, Hk, D, generator=g), torch.randn(1, N1, Hk, D, generator=g)
+    kt, vt = torch.randn(1, M, Hk, D, generator=g), torch.randn(1, M, Hk, D, generator=g)
+    k1 = torch.cat([kp, kt], 1).transpose(1, 2).contiguous()
+    v1 = torch.cat([vp, vt], 1).transpose(1, 2).contiguous()
+    mask1 = rc.additive_tree_mask(torch.from_numpy(oa.ancestor_mask(parent)))
+    c1_us, n_c1, _ = _cpu_median_us(lambda: rc.hybrid_verify_cpu(q1, k1, v1, N1, mask1), 3.0, 20)
+    return {"value": attn_us, "unit": "us/verify-step", "cores": cores,
             "affinity_cores": affinity, "threads": torch.get_num_threads(), "kind": "port",
-            "sample": f"{len(times)} full verify steps (1 layer, N={n_prefix}, M={M}, fp32 upcast), "
-                      f"median"}, out
+            "sample": f"{n_attn} full verify steps (1 layer, N={n_prefix}, M={M}, bf16 inputs upcast to fp32), "
+                      f"median",
+            "greedy_walk_us": round(walk_us, 1),
+            "greedy_walk_sample": f"{n_walk} walks over [1, {M}, {V}] fp32 N(0, 3) logits (seed 1), median",
+            "value_with_walk_us": round(attn_us + walk_us, 1),
+            "config_4096_fp32": {"attention_us": round(c1_us, 1), "greedy_walk_us": round(walk_us, 1),
+                                 "total_us": round(c1_us + walk_us, 1),
+                                 "sample": f"{n_c1} verify steps (1 layer, N=4096, M=64, fp32 N(0, 1), seed 0), "
+                                           f"median; the walk as above"}}, out
 
 
 def main():
@@ -567,6 +674,8 @@ def main():
     if not args.no_accept:
         print("[bench] acceptance kernel", file=sys.stderr, flush=True)
         line["acceptance"] = bench_accept(args, lib, ev)
+        print("[bench] fp32 4096-token layer", file=sys.stderr, flush=True)
+        line["config_4096_fp32"] = bench_fp32_4k()
     if not args.no_cpu:
         print("[bench] CPU baseline", file=sys.stderr, flush=True)
         cb, _ = cpu_baseline(inp, args)

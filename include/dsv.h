@@ -223,10 +223,14 @@ int dsv_tree_verify(const dsv_tensor* q, const dsv_tensor* k,
  * needs more fail with DSV_ERR_UNSUPPORTED (dsv_attn_workspace_bytes gives
  * the need; at head_dim 128 with 8 KV heads on 256 CUs: one tree of <= 64
  * nodes up to 512K prefix tokens, <= 128 nodes up to 256K, <= 256 nodes up
- * to 128K, 8 trees of 64 nodes at 64K).  The call allocates nothing.  Every
- * call on one
- * GPU shares that GPU's array: calls that overlap in time on one GPU (other
- * streams, other threads) race and must be serialised by the caller.
+ * to 128K, 8 trees of 64 nodes at 64K).  The call allocates nothing (its
+ * first call on a GPU looks the array's address up and creates one event).
+ * Every call on one GPU shares that GPU's array.  Calls issued on different
+ * streams are serialised by the library: a call on another stream than the
+ * previous one makes its stream wait for the previous call's kernels.
+ * Under stream capture this ordering is not added (the captured kernels run
+ * when the graph is replayed): replays of graphs holding this call, and
+ * direct calls, must not overlap in time on one GPU; the caller orders them.
  * Arguments and results are those of dsv_tree_verify.
  */
 #define DSV_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)

@@ -718,7 +718,7 @@ __global__ void __launch_bounds__(1024) accept_walk_kernel(const AcceptArgs a) {
     }
     okv[i] = recheck ? 2 : ok;
   }
-  if (__syncthreads_or(recheck)) {
+  if (a.mode == 1 && __syncthreads_or(recheck)) {  // a.mode is uniform
     // The flagged nodes' draft-token logits (lz is not read again).
     if (recheck) lz[i] = xtok;
     __syncthreads();
@@ -892,9 +892,12 @@ __global__ void __launch_bounds__(kRowThreads) accept_combine_kernel(const Accep
 
 size_t accept_walk_lds_bytes(int M);
 
-// The walk runs one thread per node, and at least 256 threads so that the
-// typical re-check streams a row with a whole workgroup.
-static int walk_threads(int M) { return std::max(256, ((M + 63) / 64) * 64); }
+// The walk runs one thread per node; in typical mode at least 256 threads,
+// so that the re-check streams a row with a whole workgroup.
+static int walk_threads(const AcceptArgs& a) {
+  const int t = ((a.M + 63) / 64) * 64;
+  return a.mode == 1 ? std::max(256, t) : t;
+}
 
 hipError_t launch_accept_from_parts(const AcceptArgs& a, const float4* part, const float* part2, int nin,
                                     hipStream_t s) {
@@ -906,7 +909,7 @@ hipError_t launch_accept_from_parts(const AcceptArgs& a, const float4* part, con
     hipLaunchKernelGGL(accept_combine_kernel<false>, grid, dim3(kRowThreads), 0, s, a, part, part2, nin);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int threads = walk_threads(a.M);
+  const int threads = walk_threads(a);
   hipLaunchKernelGGL(accept_walk_kernel, dim3((unsigned)a.T), dim3(threads), accept_walk_lds_bytes(a.M), s, a);
   return hipGetLastError();
 }
@@ -959,7 +962,7 @@ hipError_t launch_accept(const AcceptArgs& a, hipStream_t s, hipEvent_t ev0, hip
 }
 
 hipError_t launch_walk(const AcceptArgs& a, hipStream_t s) {
-  const int threads = walk_threads(a.M);
+  const int threads = walk_threads(a);
   hipLaunchKernelGGL(accept_walk_kernel, dim3((unsigned)a.T), dim3(threads), accept_walk_lds_bytes(a.M), s, a);
   return hipGetLastError();
 }

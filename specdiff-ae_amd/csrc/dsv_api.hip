@@ -100,20 +100,22 @@ int check_nd(const dsv_tensor* t, const char* name, int ndim) {
   return DSV_OK;
 }
 
-// 16-bit operand read with 16-byte vector loads: innermost stride 1, other
-// strides multiples of 8 elements, 16-byte aligned base.
+// Attention operand (q, k, v, pages) read with 16-byte vector loads: bf16,
+// f16 or f32; innermost stride 1, other strides multiples of 16 bytes,
+// 16-byte aligned base.
 int check_vec16(const dsv_tensor* t, const char* name, int skip_dim = -1) {
-  if (t->dtype != DSV_BF16 && t->dtype != DSV_F16)
-    return fail(DSV_ERR_UNSUPPORTED, "%s: dtype %s is not supported by the MI355X kernels (bf16 or f16 required)",
+  if (t->dtype != DSV_BF16 && t->dtype != DSV_F16 && t->dtype != DSV_F32)
+    return fail(DSV_ERR_UNSUPPORTED, "%s: dtype %s is not supported by the MI355X kernels (bf16, f16 or f32)",
                 name, dt_name(t->dtype));
+  const int per16 = 16 / elem_size(t->dtype);  // elements per 16 bytes
   if (t->stride[t->ndim - 1] != 1) return fail(DSV_ERR_INVALID, "%s: innermost stride must be 1", name);
   if ((reinterpret_cast<uintptr_t>(t->data) & 15) != 0)
     return fail(DSV_ERR_INVALID, "%s: data pointer must be 16-byte aligned", name);
   for (int i = 0; i < t->ndim - 1; ++i) {
     if (i == skip_dim) continue;
-    if (t->shape[i] > 1 && (t->stride[i] % 8) != 0)
-      return fail(DSV_ERR_INVALID, "%s: stride[%d]=%lld is not a multiple of 8 elements", name, i,
-                  (long long)t->stride[i]);
+    if (t->shape[i] > 1 && (t->stride[i] % per16) != 0)
+      return fail(DSV_ERR_INVALID, "%s: stride[%d]=%lld is not a multiple of %d elements (16 bytes)", name, i,
+                  (long long)t->stride[i], per16);
   }
   return DSV_OK;
 }
@@ -302,14 +304,15 @@ int run(const AttnArgs& a_in, const MergeArgs& m, int dtype, int D, bool dmask, 
   if (g_dry_run) {
     std::string err;
     int64_t n = 0;
-    const int rc = dsv::emulate_attention(a, m, D, dmask, ex, err, &n);
+    const int rc = dsv::emulate_attention(a, m, D, dmask, dtype == DSV_F32, ex, err, &n);
     g_dry_checks = n;
     if (rc != 0) return fail(DSV_ERR_INVALID, "dry run: out-of-bounds access: %s", err.c_str());
     return DSV_OK;
   }
   hipEvent_t ev0, ev1;
   take_events(ev0, ev1);
-  hipError_t e = dsv::launch_attn(a, dtype, D, dmask, st, ev0, ev1);
+  hipError_t e = dtype == DSV_F32 ? dsv::launch_attn_f32(a, D, dmask, st, ev0, ev1)
+                                  : dsv::launch_attn(a, dtype, D, dmask, st, ev0, ev1);
   if (e != hipSuccess) return hip_fail(e, "attention kernel launch");
   e = dsv::launch_merge(m, st);
   if (e != hipSuccess) return hip_fail(e, "merge kernel launch");
@@ -346,9 +349,10 @@ int paged_src(const dsv_tensor* kv_pages, int64_t layer, const dsv_tensor* pt, i
   if (pt->stride[pt->ndim - 1] != 1) return fail(DSV_ERR_INVALID, "page_table innermost stride must be 1");
   Hk = kv_pages->shape[3];
   D = kv_pages->shape[5];
-  const char* base = static_cast<const char*>(kv_pages->data) + layer * kv_pages->stride[0] * 2;
+  const int es = elem_size(kv_pages->dtype);
+  const char* base = static_cast<const char*>(kv_pages->data) + layer * kv_pages->stride[0] * es;
   s.k = reinterpret_cast<const uint16_t*>(base);
-  s.v = reinterpret_cast<const uint16_t*>(base + kv_pages->stride[1] * 2);
+  s.v = reinterpret_cast<const uint16_t*>(base + kv_pages->stride[1] * es);
   s.k_sb = s.v_sb = 0;
   s.k_sp = s.v_sp = kv_pages->stride[2];
   s.k_sh = s.v_sh = kv_pages->stride[3];
@@ -635,26 +639,41 @@ static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
-void* g_scratch_ptr[kMaxDevices] = {};
 
-// Device address of this GPU's scratch array, looked up once per device with
-// that device current (the array's name is a host-side stand-in and may not
-// be passed to a kernel or a copy).
-int scratch_for_current_device(void** ptr) {
+// Per GPU: the scratch array's device address, and the guard that orders
+// calls made on different streams: an event recorded after each call's
+// kernels and the stream it was recorded on.  A call on another stream first
+// makes its stream wait for that event, so two calls never use the array at
+// the same time unless a caller hides them from the guard (graph capture,
+// see dsv.h).
+struct NoAllocDevice {
+  void* scratch = nullptr;
+  hipEvent_t done = nullptr;
+  hipStream_t last = nullptr;
+  bool used = false;
+};
+NoAllocDevice g_noalloc[kMaxDevices];
+
+// Set-up, once per device with that device current: the scratch array's
+// address (its name is a host-side stand-in and may not be passed to a
+// kernel or a copy) and the guard's event.  Called with g_scratch_mu held.
+int noalloc_device(NoAllocDevice** out) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
   if (dev < 0 || dev >= kMaxDevices) return fail(DSV_ERR_UNSUPPORTED, "device ordinal %d beyond %d", dev, kMaxDevices);
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (g_scratch_ptr[dev] == nullptr) {
+  NoAllocDevice& d = g_noalloc[dev];
+  if (d.scratch == nullptr) {
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
     if (p == nullptr || (reinterpret_cast<uintptr_t>(p) & 255) != 0)
       return fail(DSV_ERR_HIP, "scratch array at an unusable address");
-    g_scratch_ptr[dev] = p;
+    e = hipEventCreateWithFlags(&d.done, hipEventDisableTiming);
+    if (e != hipSuccess) return hip_fail(e, "hipEventCreateWithFlags (allocation-free entry point set-up)");
+    d.scratch = p;
   }
-  *ptr = g_scratch_ptr[dev];
+  *out = &d;
   return DSV_OK;
 }
 
@@ -732,14 +751,28 @@ int tree_verify_impl(const dsv_tensor* q, const dsv_tensor* k, const dsv_tensor*
       return fail(DSV_ERR_INVALID, "lse must be float32 [B, M, H]");
   }
   const Plan p = make_plan(B, M, H, Hk, D, n_prefix, ps, true);
+  // The allocation-free entry point holds g_scratch_mu from here to the end
+  // of its launches, so that the guard's wait, the kernels and the record of
+  // the guard's event are one step for other threads.
+  std::unique_lock<std::mutex> lock(g_scratch_mu, std::defer_lock);
+  NoAllocDevice* nad = nullptr;
+  bool guard = false;
   if (noalloc) {
     if (p.total > kNoAllocScratchBytes)
       return fail(DSV_ERR_UNSUPPORTED,
                   "this shape needs %zu bytes of split scratch, above the %zu bytes of the allocation-free entry "
                   "point; use dsv_tree_verify with a workspace",
                   p.total, kNoAllocScratchBytes);
-    if ((rc = scratch_for_current_device(&workspace)) != DSV_OK) return rc;
+    lock.lock();
+    if ((rc = noalloc_device(&nad)) != DSV_OK) return rc;
+    workspace = nad->scratch;
     workspace_bytes = kNoAllocScratchBytes;
+    // Under stream capture the guard stands aside: the captured kernels run
+    // when the graph is replayed, in the order the caller gives the replays.
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    hipError_t e = hipStreamIsCapturing(static_cast<hipStream_t>(stream), &cs);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
+    guard = cs == hipStreamCaptureStatusNone && !g_dry_run;
   }
   if ((rc = check_ws(p, workspace, workspace_bytes)) != DSV_OK) return rc;
 
@@ -771,7 +804,20 @@ int tree_verify_impl(const dsv_tensor* q, const dsv_tensor* k, const dsv_tensor*
   ex.tpar = extent_of("parent", parent);
   ex.perm = extent_of("row_perm", row_perm);
   ex.lse = extent_of("lse", lse);
-  return run(a, m, q->dtype, (int)D, false, static_cast<hipStream_t>(stream), ex);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (guard && nad->used && nad->last != st) {
+    // The previous call ran on another stream: this one starts after it.
+    const hipError_t e = hipStreamWaitEvent(st, nad->done, 0);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamWaitEvent (allocation-free entry point guard)");
+  }
+  rc = run(a, m, q->dtype, (int)D, false, st, ex);
+  if (rc == DSV_OK && guard) {
+    const hipError_t e = hipEventRecord(nad->done, st);
+    if (e != hipSuccess) return hip_fail(e, "hipEventRecord (allocation-free entry point guard)");
+    nad->last = st;
+    nad->used = true;
+  }
+  return rc;
 }
 
 }  // namespace

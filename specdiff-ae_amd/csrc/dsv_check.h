@@ -26,8 +26,9 @@ struct AttnExtents {
 };
 
 // 0 when every access of kernels 1 and 3 stays inside its extent; otherwise
-// -1 with a description of the first violation in `err`.
-int emulate_attention(const AttnArgs& a, const MergeArgs& m, int D, bool dmask, const AttnExtents& ex,
+// -1 with a description of the first violation in `err`.  f32: the fp32
+// variant of kernel 1 (dsv_attn_f32.hip).
+int emulate_attention(const AttnArgs& a, const MergeArgs& m, int D, bool dmask, bool f32, const AttnExtents& ex,
                       std::string& err, int64_t* n_checked);
 
 }  // namespace dsv

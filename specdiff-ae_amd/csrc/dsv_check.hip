@@ -12,6 +12,7 @@
 #include <cstdio>
 #include <string>
 
+#include "dsv_attn_f32_geo.h"
 #include "dsv_attn_geo.h"
 #include "dsv_check.h"
 
@@ -192,6 +193,92 @@ void check_kernel1(const AttnArgs& a, bool dmask, const AttnExtents& ex, Checker
   }
 }
 
+// The fp32 kernel: per workgroup, the page-table slice and tree inputs as in
+// the 16-bit kernel; per tile, every thread's 16-byte K and V chunk loads
+// (keys clamped to the split, pages at both ends of the clamp range); the Q
+// rows (fp32) and the bf16 partial rows it writes.
+template <int D>
+void check_kernel_f32(const AttnArgs& a, bool dmask, const AttnExtents& ex, Checker& ck) {
+  using G = GeoF32<D>;
+  const int64_t nrows_all = (int64_t)a.s_total * a.B * a.Hk * a.R;
+  for (int b = 0; b < a.B && ck.ok; ++b) {
+    for (int kvh = 0; kvh < a.Hk && ck.ok; ++kvh) {
+      for (int split = 0; split < a.s_total && ck.ok; ++split) {
+        const bool is_tree = a.has_tree && split == a.n_splits;
+        const KvSrc& src = is_tree ? a.tree : a.pre;
+        const Extent& ek = is_tree ? ex.tree_k : ex.pre_k;
+        const Extent& ev = is_tree ? ex.tree_v : ex.pre_v;
+        const Extent& ept = is_tree ? ex.tree_pt : ex.pre_pt;
+        int64_t kstart, kend;
+        if (is_tree) {
+          kstart = 0;
+          kend = a.M;
+        } else {
+          kstart = (int64_t)split * a.kps;
+          kend = std::min(kstart + a.kps, a.n_pre);
+        }
+        const int64_t nkeys = kend - kstart;
+        const int ntiles = nkeys > 0 ? (int)((nkeys + G::KT - 1) / G::KT) : 0;
+        const bool paged = src.pt != nullptr;
+        int64_t pt_lo = 0;
+        if (paged && ntiles > 0) {
+          pt_lo = (src.key0 + kstart) >> src.ps_shift;
+          const int64_t pt_hi = (src.key0 + kend - 1) >> src.ps_shift;
+          ck.cond(pt_hi - pt_lo + 1 <= kPageLds, "page-table slice exceeds its LDS table");
+          const int es = src.pt_i64 ? 8 : 4;
+          ck.range(ept, elem_addr(src.pt, b * src.pt_sb + pt_lo, es), (pt_hi - pt_lo + 1) * es, "page-table read");
+          ck.cond(src.n_phys > 0, "empty page pool");
+        }
+        if (is_tree) {
+          ck.cond(a.M <= kTreeMaxM, "tree larger than the LDS bitmask table");
+          if (a.tpar != nullptr) {
+            const int es = a.tpar_i64 ? 8 : 4;
+            for (int node = 0; node < a.M; ++node)
+              ck.range(ex.tpar, elem_addr(a.tpar, b * a.tpar_sb + node * a.tpar_sm, es), es, "parent read");
+          } else {
+            const int es = a.tmask_dtype == 2 ? 4 : (a.tmask_dtype <= 1 ? 2 : 1);
+            const int64_t last = b * a.tm_sb + (int64_t)(a.M - 1) * a.tm_sm + (int64_t)(a.M - 1) * a.tm_sn;
+            ck.range(ex.tmask, elem_addr(a.tmask, b * a.tm_sb, es), 1, "tree-mask read (first)");
+            ck.range(ex.tmask, elem_addr(a.tmask, last, es), es, "tree-mask read (last)");
+          }
+        }
+        const int64_t pages[2] = {0, paged ? src.n_phys - 1 : 0};
+        for (int t = 0; t < ntiles && ck.ok; ++t) {
+          const int64_t kb = kstart + (int64_t)t * G::KT;
+          for (int ch = 0; ch < G::CHUNKS && ck.ok; ++ch) {
+            const int kk = ch / G::CPR, c4 = ch % G::CPR;
+            const int64_t n = f32_key(src, kb, kend, kk);
+            ck.cond(!paged || ((n >> src.ps_shift) - pt_lo >= 0 && (n >> src.ps_shift) - pt_lo < kPageLds),
+                    "page slot outside the staged slice");
+            for (int pi = 0; pi < (paged ? 2 : 1); ++pi) {
+              ck.range(ek, elem_addr(src.k, f32_elem(src, false, b, kvh, n, pages[pi], c4), 4), 16, "K load (f32)");
+              ck.range(ev, elem_addr(src.v, f32_elem(src, true, b, kvh, n, pages[pi], c4), 4), 16, "V load (f32)");
+            }
+          }
+          if (dmask && a.dmask != nullptr) {
+            const int64_t nmax = std::min(kb + G::KT, a.dm_n) - 1;
+            if (nmax >= 0 && nmax >= kb) {
+              const int64_t last = b * a.dm_sb + (int64_t)(a.M - 1) * a.dm_sm + nmax * a.dm_sn;
+              ck.range(ex.dmask, elem_addr(a.dmask, last, 1), 1, "byte-mask read");
+              ck.range(ex.dmask, elem_addr(a.dmask, b * a.dm_sb + kb * a.dm_sn, 1), 1, "byte-mask read");
+            }
+          }
+        }
+        for (int r = 0; r < a.R && ck.ok; ++r) {
+          const int g = r / a.M, mi = r - g * a.M;
+          ck.range(ex.q, elem_addr(a.q, b * a.q_sb + (int64_t)mi * a.q_sm + (int64_t)(kvh * a.G + g) * a.q_sh, 4),
+                   4 * D, "Q row read (f32)");
+          if (a.row_perm != nullptr) ck.range(ex.perm, elem_addr(a.row_perm, mi, 4), 4, "row_perm read");
+          const int64_t prow = (((int64_t)split * a.B + b) * a.Hk + kvh) * a.R + r;
+          ck.cond(prow < nrows_all, "partial row out of range");
+          ck.range(ex.ws, elem_addr(a.opart, prow * D, 2), 2 * D, "partial write");
+          ck.range(ex.ws, (uintptr_t)(a.ml + prow), 8, "partial stats write");
+        }
+      }
+    }
+  }
+}
+
 void check_merge(const MergeArgs& m, const AttnExtents& ex, Checker& ck) {
   const int64_t nrows = (int64_t)m.B * m.Hk * m.R;
   for (int64_t row = 0; row < nrows && ck.ok; ++row) {
@@ -225,13 +312,13 @@ void check_merge(const MergeArgs& m, const AttnExtents& ex, Checker& ck) {
 
 }  // namespace
 
-int emulate_attention(const AttnArgs& a, const MergeArgs& m, int D, bool dmask, const AttnExtents& ex,
+int emulate_attention(const AttnArgs& a, const MergeArgs& m, int D, bool dmask, bool f32, const AttnExtents& ex,
                       std::string& err, int64_t* n_checked) {
   Checker ck{&err};
   if (D == 128)
-    check_kernel1<128>(a, dmask, ex, ck);
+    f32 ? check_kernel_f32<128>(a, dmask, ex, ck) : check_kernel1<128>(a, dmask, ex, ck);
   else if (D == 64)
-    check_kernel1<64>(a, dmask, ex, ck);
+    f32 ? check_kernel_f32<64>(a, dmask, ex, ck) : check_kernel1<64>(a, dmask, ex, ck);
   else
     ck.cond(false, "unsupported head_dim in emulation");
   if (ck.ok) check_merge(m, ex, ck);

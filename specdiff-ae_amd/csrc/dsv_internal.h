@@ -217,6 +217,9 @@ struct LmArgs {
 // end times.
 hipError_t launch_attn(const AttnArgs& a, int dtype, int D, bool dmask, hipStream_t s, hipEvent_t ev0 = nullptr,
                        hipEvent_t ev1 = nullptr);
+// The fp32 variant (same plan, masks and partial format; dsv_attn_f32.hip).
+hipError_t launch_attn_f32(const AttnArgs& a, int D, bool dmask, hipStream_t s, hipEvent_t ev0 = nullptr,
+                           hipEvent_t ev1 = nullptr);
 // What the host plan needs from the attention kernel's workgroup shape.
 int attn_rows_per_block();
 int attn_blocks_per_cu();

@@ -23,8 +23,8 @@ LIB_DIR = PKG_DIR / "_lib"
 LIB_PATH = LIB_DIR / "libdsv.so"
 OBJ_DIR = LIB_DIR / "obj"
 
-SOURCES = ["dsv_attn.hip", "dsv_merge.hip", "dsv_accept.hip", "dsv_sample.hip", "dsv_commit.hip", "dsv_append.hip", "dsv_bundle.hip", "dsv_lmhead.hip", "dsv_check.hip", "dsv_api.hip"]
-HEADERS = ["dsv_internal.h", "dsv_attn_geo.h", "dsv_check.h", "dsv_stats.h", "dsv_dma.h"]
+SOURCES = ["dsv_attn.hip", "dsv_attn_f32.hip", "dsv_merge.hip", "dsv_accept.hip", "dsv_sample.hip", "dsv_commit.hip", "dsv_append.hip", "dsv_bundle.hip", "dsv_lmhead.hip", "dsv_check.hip", "dsv_api.hip"]
+HEADERS = ["dsv_internal.h", "dsv_attn_geo.h", "dsv_attn_f32_geo.h", "dsv_check.h", "dsv_stats.h", "dsv_dma.h"]
 
 ARCH = "gfx950"
 COMMON_FLAGS = [

@@ -231,10 +231,13 @@ class LlamaVerifyStep:
         tf = t.float()
         return (tf * torch.rsqrt(tf.pow(2).mean(-1, keepdim=True) + 1e-5)).to(torch.bfloat16)
 
-    def hidden(self, capture: Sequence[int] = ()) -> Tuple[torch.Tensor, Dict[int, Tuple[torch.Tensor, torch.Tensor]]]:
+    def hidden(self, capture: Sequence[int] = (), verify_hook=None
+               ) -> Tuple[torch.Tensor, Dict[int, Tuple[torch.Tensor, torch.Tensor]]]:
         """The 32 layers over the tree; returns the final normed hidden states
         [M, hidden] and, for the layers in ``capture``, (rotated q [M, H, D],
-        attention output [M, H, D])."""
+        attention output [M, H, D]).  ``verify_hook(layer, phase)``, when
+        given, is called right before (phase 0) and right after (phase 1)
+        each layer's fused tree verify (a measurement hook)."""
         from .runtime.cache_state import append_tree_kv
         from .runtime.tree_attention import tree_verify
 
@@ -248,8 +251,12 @@ class LlamaVerifyStep:
             q = append_tree_kv(qkv[:, H * D:(H + Hk) * D].view(M, Hk, D), qkv[:, (H + Hk) * D:].view(M, Hk, D),
                                inp.kv_pages[l, 0], inp.kv_pages[l, 1], N, cos=self.cos, sin=self.sin,
                                page_table=inp.page_table, q=qkv[:, :H * D].view(M, H, D))
+            if verify_hook is not None:
+                verify_hook(l, 0)
             o, _ = tree_verify(q.unsqueeze(0), inp.kv_pages[l, 0], inp.kv_pages[l, 1], N, self.par,
                                page_table=inp.page_table)
+            if verify_hook is not None:
+                verify_hook(l, 1)
             if l in capture:
                 caps[l] = (q.clone(), o[0].clone())
             x = x + o.view(M, H * D) @ W["o"].T
@@ -257,12 +264,12 @@ class LlamaVerifyStep:
             x = x + (torch.nn.functional.silu(gu[:, :F].float()) * gu[:, F:].float()).to(torch.bfloat16) @ W["d"].T
         return self.rms(x), caps
 
-    def step(self) -> Dict[str, torch.Tensor]:
+    def step(self, verify_hook=None) -> Dict[str, torch.Tensor]:
         """The whole verification step: layers, then the lm_head fused with the
         greedy walk (kernel 5 + kernel 4's walk)."""
         from .draft.tree_verification import lmhead_tree_accept
 
-        xn, _ = self.hidden()
+        xn, _ = self.hidden(verify_hook=verify_hook)
         return lmhead_tree_accept(xn.unsqueeze(0), self.lm_head, self.draft, self.pref, self.pos, self.max_hops)
 
     def torch_logits(self, xn: torch.Tensor) -> torch.Tensor:

@@ -100,10 +100,14 @@ def test_validation_errors_are_reported(dsv_lib):
     rc = dsv_lib.dsv_prefix_attention_forward(ctypes.byref(q), ctypes.byref(k), ctypes.byref(k), -1,
                                               ctypes.byref(out), ctypes.byref(lse_bad), None, 0, None)
     assert rc == -1 and "lse" in _ext.last_error()
-    q32 = _t((1, 4, 8, 128), _ext.DSV_F32)
+    q8 = _t((1, 4, 8, 128), _ext.DSV_I8)
+    rc = dsv_lib.dsv_prefix_attention_forward(ctypes.byref(q8), ctypes.byref(k), ctypes.byref(k), -1,
+                                              ctypes.byref(out), ctypes.byref(lse_bad), None, 0, None)
+    assert rc == -2 and "bf16, f16 or f32" in _ext.last_error()
+    q32 = _t((1, 4, 8, 128), _ext.DSV_F32)  # fp32 q with bf16 keys: the dtypes must agree
     rc = dsv_lib.dsv_prefix_attention_forward(ctypes.byref(q32), ctypes.byref(k), ctypes.byref(k), -1,
                                               ctypes.byref(out), ctypes.byref(lse_bad), None, 0, None)
-    assert rc == -2 and "bf16" in _ext.last_error()
+    assert rc == -1 and "dtype" in _ext.last_error()
     q96 = _t((1, 4, 8, 96))
     rc = dsv_lib.dsv_prefix_attention_forward(ctypes.byref(q96), ctypes.byref(k), ctypes.byref(k), -1,
                                               ctypes.byref(q96), ctypes.byref(lse_bad), None, 0, None)

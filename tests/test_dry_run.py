@@ -77,10 +77,11 @@ def ok(lib, rc, what):
 @pytest.mark.parametrize("D,H,Hk,M,N,B", [(128, 32, 8, 64, 1000, 2), (64, 8, 8, 10, 20, 1), (128, 32, 8, 5, 4096, 1),
                                          (64, 16, 4, 33, 777, 1), (128, 8, 2, 16, 300, 1),
                                          (128, 16, 4, 24, 3000, 1), (128, 16, 4, 24, 20000, 1)])
-def test_prefix_attention(dry, D, H, Hk, M, N, B):
+@pytest.mark.parametrize("dt", [_ext.DSV_BF16, _ext.DSV_F32])
+def test_prefix_attention(dry, D, H, Hk, M, N, B, dt):
     a = Alloc()
-    q, k, v = tensor(a, (B, M, H, D)), tensor(a, (B, N, Hk, D)), tensor(a, (B, N, Hk, D))
-    out, lse = tensor(a, (B, M, H, D)), tensor(a, (B, H, M), _ext.DSV_F32)
+    q, k, v = tensor(a, (B, M, H, D), dt), tensor(a, (B, N, Hk, D), dt), tensor(a, (B, N, Hk, D), dt)
+    out, lse = tensor(a, (B, M, H, D), dt), tensor(a, (B, H, M), _ext.DSV_F32)
     ws = dry.dsv_attn_workspace_bytes(B, M, H, Hk, D, N, 0, 0)
     wsp = a.take(ws)
     for nk in (-1, N // 3):
@@ -90,13 +91,14 @@ def test_prefix_attention(dry, D, H, Hk, M, N, B):
 
 
 @pytest.mark.parametrize("mask_dtype", [_ext.DSV_F32, _ext.DSV_I8, _ext.DSV_BOOL, _ext.DSV_BF16])
-def test_tree_attention_forward(dry, mask_dtype):
+@pytest.mark.parametrize("dt", [_ext.DSV_BF16, _ext.DSV_F32])
+def test_tree_attention_forward(dry, mask_dtype, dt):
     a = Alloc()
     B, M, H, Hk, D, T = 2, 64, 32, 8, 128, 70
-    q, k, v = tensor(a, (B, M, H, D)), tensor(a, (B, M, Hk, D)), tensor(a, (B, M, Hk, D))
+    q, k, v = tensor(a, (B, M, H, D), dt), tensor(a, (B, M, Hk, D), dt), tensor(a, (B, M, Hk, D), dt)
     mask = tensor(a, (B, 1, T, T), mask_dtype)
     plse = tensor(a, (B, H, M), _ext.DSV_F32)
-    cur, w, tl = tensor(a, (B, M, H, D)), tensor(a, (B, M, H, 1)), tensor(a, (B, M, H), _ext.DSV_F32)
+    cur, w, tl = tensor(a, (B, M, H, D), dt), tensor(a, (B, M, H, 1), dt), tensor(a, (B, M, H), _ext.DSV_F32)
     ws = dry.dsv_attn_workspace_bytes(B, M, H, Hk, D, 0, 0, 1)
     rc = dry.dsv_tree_attention_forward(ctypes.byref(q), ctypes.byref(k), ctypes.byref(v), ctypes.byref(mask),
                                         ctypes.byref(plse), ctypes.byref(cur), ctypes.byref(w), ctypes.byref(tl),
@@ -104,10 +106,10 @@ def test_tree_attention_forward(dry, mask_dtype):
     ok(dry, rc, "tree_attention_forward")
 
 
-def paged_case(a, n_tok, Hk=8, D=128, ps=16, layers=1, spare=0):
+def paged_case(a, n_tok, Hk=8, D=128, ps=16, layers=1, spare=0, dt=_ext.DSV_BF16):
     n_pages = (n_tok + ps - 1) // ps
     P = n_pages + spare
-    pool = tensor(a, (layers, 2, P, Hk, ps, D))
+    pool = tensor(a, (layers, 2, P, Hk, ps, D), dt)
     pt = tensor(a, (n_pages,), _ext.DSV_I32)
     return pool, pt, P
 
@@ -158,6 +160,35 @@ def test_tree_verify_paged_and_dense(dry, n_prefix, M, ps, H, Hk, D, perm):
     ok(dry, rc, "tree_verify dense")
 
 
+@pytest.mark.parametrize("n_prefix,M,ps,H,Hk,D,perm", [
+    (4096, 64, 16, 32, 8, 128, False), (0, 64, 16, 32, 8, 128, False), (100, 7, 16, 32, 8, 128, True),
+    (1000, 64, 1, 8, 2, 128, False), (1000, 64, 4, 8, 2, 64, False), (1000, 64, 64, 8, 2, 128, True),
+    (6000, 256, 16, 32, 8, 128, False), (30000, 192, 16, 32, 8, 128, False)])
+def test_tree_verify_paged_and_dense_f32(dry, n_prefix, M, ps, H, Hk, D, perm):
+    """The fp32 kernel's loads, over the shapes the fp32 GPU tests launch."""
+    a = Alloc()
+    B, dt = 1, _ext.DSV_F32
+    q = tensor(a, (B, M, H, D), dt)
+    pool, pt, P = paged_case(a, n_prefix + M, Hk=Hk, D=D, ps=ps, layers=2, spare=3, dt=dt)
+    par = tensor(a, (M,), _ext.DSV_I64)
+    rp = tensor(a, (M,), _ext.DSV_I32) if perm else none()
+    out, lse = tensor(a, (B, M, H, D), dt), tensor(a, (B, M, H), _ext.DSV_F32)
+    ws = dry.dsv_attn_workspace_bytes(B, M, H, Hk, D, n_prefix, ps, 1)
+    wsp = a.take(ws)
+    for layer in (0, 1):
+        kh, vh = pool_half(pool, layer, 0), pool_half(pool, layer, 1)
+        rc = dry.dsv_tree_verify(ctypes.byref(q), ctypes.byref(kh), ctypes.byref(vh), ctypes.byref(pt), n_prefix,
+                                 ctypes.byref(par), ctypes.byref(rp), ctypes.byref(out), ctypes.byref(lse), wsp, ws,
+                                 None)
+        ok(dry, rc, f"tree_verify paged f32 layer {layer}")
+    kc, vc = tensor(a, (B, n_prefix + M, Hk, D), dt), tensor(a, (B, n_prefix + M, Hk, D), dt)
+    ws2 = dry.dsv_attn_workspace_bytes(B, M, H, Hk, D, n_prefix, 0, 1)
+    rc = dry.dsv_tree_verify(ctypes.byref(q), ctypes.byref(kc), ctypes.byref(vc), ctypes.byref(none()), n_prefix,
+                             ctypes.byref(par), ctypes.byref(rp), ctypes.byref(out), ctypes.byref(lse), a.take(ws2),
+                             ws2, None)
+    ok(dry, rc, "tree_verify dense f32")
+
+
 def test_bench_shape_with_rotated_layers(dry):
     a = Alloc()
     n_prefix, M, H, Hk, D = 65536, 64, 32, 8, 128
@@ -176,16 +207,17 @@ def test_bench_shape_with_rotated_layers(dry):
 
 
 @pytest.mark.parametrize("B,M,H,Hk,D,N", [(1, 10, 8, 8, 64, 20), (1, 12, 8, 2, 128, 300), (2, 40, 32, 8, 128, 1000)])
-def test_verify_bundle_dense_and_paged(dry, B, M, H, Hk, D, N):
+@pytest.mark.parametrize("dt", [_ext.DSV_BF16, _ext.DSV_F32])
+def test_verify_bundle_dense_and_paged(dry, B, M, H, Hk, D, N, dt):
     a = Alloc()
-    q, k, v = tensor(a, (B, M, H, D)), tensor(a, (B, N, Hk, D)), tensor(a, (B, N, Hk, D))
+    q, k, v = tensor(a, (B, M, H, D), dt), tensor(a, (B, N, Hk, D), dt), tensor(a, (B, N, Hk, D), dt)
     mask = tensor(a, (1, M, N), _ext.DSV_I8)
-    out, lse = tensor(a, (B, M, H, D)), tensor(a, (B, M, H), _ext.DSV_F32)
+    out, lse = tensor(a, (B, M, H, D), dt), tensor(a, (B, M, H), _ext.DSV_F32)
     ws = dry.dsv_attn_workspace_bytes(B, M, H, Hk, D, N, 0, 0)
     rc = dry.dsv_verify_bundle(ctypes.byref(q), ctypes.byref(k), ctypes.byref(v), ctypes.byref(mask), ctypes.byref(out),
                                ctypes.byref(lse), a.take(ws), ws, None)
     ok(dry, rc, "verify_bundle")
-    pool, pt, P = paged_case(a, N, Hk=Hk, D=D, ps=16, layers=2, spare=3)
+    pool, pt, P = paged_case(a, N, Hk=Hk, D=D, ps=16, layers=2, spare=3, dt=dt)
     ws = dry.dsv_attn_workspace_bytes(B, M, H, Hk, D, N, 16, 0)
     rc = dry.dsv_verify_bundle_paged(ctypes.byref(q), ctypes.byref(pool), ctypes.byref(pt), 1, ctypes.byref(mask),
                                      ctypes.byref(out), ctypes.byref(lse), a.take(ws), ws, None)

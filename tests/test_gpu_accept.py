@@ -248,14 +248,16 @@ def test_packed_key_sweep_strided_rows_with_short_tail(gpu):
                     posterior_threshold=0.09, posterior_alpha=0.3)
 
 
-def test_verify_new_takes_the_reference_copy_beyond_the_commit_kernel_limit(gpu):
-    """A 300-node tree with 128-element fp32 cache rows (300 x 512 B above the
-    commit kernel's 64 KiB of staged tree rows) takes the reference's gather +
-    copy instead of raising."""
-    M = 300
+@pytest.mark.parametrize("M", [200, 300])
+def test_verify_new_takes_the_reference_copy_beyond_the_commit_kernel_limit(gpu, M):
+    """A 200- or 300-node tree with 128-element fp32 cache rows (M x 512 B,
+    above the commit kernel's 64 KiB of staged tree rows) takes the
+    reference's gather + copy instead of raising, with the same result."""
+    from diffspec_mi355x.draft.tree_verification import _kv_commit_ok
     a = wl.make_accept_inputs(T=1, M=M, V=3000, device=str(gpu), seed=3, max_outdeg=6, pos_offset=50)
     L = M + 40
     kv = [torch.randn(2, 1, 2, L, 128, device=gpu) for _ in range(2)]
+    assert not _kv_commit_ok(kv[0], M)             # the fallback branch is the one taken
     kv_before = [x.clone() for x in kv]
     cur_len = torch.tensor([L], dtype=torch.long)
     start = L - M

@@ -178,3 +178,35 @@ def test_sample_walk_follows_the_greedy_rule_with_the_draws():
     onehot[np.arange(M), draws] = 1.0
     assert res[:5] == oacc.greedy_walk(onehot, draft, pref, pos, 8)
     assert res[1][:6] == [0, 1, 2, 3, 8, 9]
+
+
+def test_reference_call_shape_and_the_per_row_rule():
+    """The reference warps the target logits as one [1, M, V] tensor
+    (draft/tree_verification.py:104).  transformers' TopPLogitsWarper scatters
+    its removal mask along dim 1, so on that shape it raises (an index out of
+    range for dimension 1): the reference's top-p branch fails there.  The temperature and top-k warpers
+    work on [1, M, V] and give exactly what they give row by row.  This build
+    defines sampling by the warpers applied to each [1, V] row, which the
+    oracle restates: checked here against transformers on every row."""
+    import torch
+    from transformers.generation.logits_process import (LogitsProcessorList, TemperatureLogitsWarper,
+                                                        TopKLogitsWarper, TopPLogitsWarper)
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn((1, 4, 50), generator=g) * 2.0
+    with pytest.raises((IndexError, RuntimeError), match="out of (range|bounds)"):
+        TopPLogitsWarper(0.9)(None, x)
+    rowwise = lambda lst, t: torch.cat([lst(None, t[:, r, :].clone()) for r in range(t.shape[1])])
+    no_p = LogitsProcessorList([TemperatureLogitsWarper(0.7), TopKLogitsWarper(5)])
+    assert torch.equal(no_p(None, x.clone())[0], rowwise(no_p, x))
+    for temperature, top_p, top_k in [(0.7, 0.9, 0), (1.0, 0.5, 7), (1.3, 0.95, 3)]:
+        lst = LogitsProcessorList()
+        if temperature != 1.0:
+            lst.append(TemperatureLogitsWarper(temperature))
+        lst.append(TopPLogitsWarper(top_p))
+        if top_k > 0:
+            lst.append(TopKLogitsWarper(top_k))
+        warped = rowwise(lst, x)
+        for r in range(x.shape[1]):
+            y = sp.warp_temperature(x[0, r].numpy(), temperature, "f32")
+            keep = sp.kept_mask(y, top_p, top_k)
+            assert np.array_equal(keep, torch.isfinite(warped[r]).numpy()), (temperature, top_p, top_k, r)

@@ -15,7 +15,7 @@ from diffspec_mi355x import workloads as wl
 pytestmark = pytest.mark.gpu
 
 
-def _verify(lib, inp, par, noalloc):
+def _verify(lib, inp, par, noalloc, stream=None):
     q = inp.q
     B, M, H, D = q.shape
     out = torch.empty((B, M, H, D), dtype=torch.float32, device=q.device)
@@ -24,7 +24,7 @@ def _verify(lib, inp, par, noalloc):
     args = [ctypes.byref(_ext.desc(x)) for x in (q, k, v, inp.page_table)]
     tail = [ctypes.byref(_ext.desc(par)), ctypes.byref(_ext.desc(None)), ctypes.byref(_ext.desc(out)),
             ctypes.byref(_ext.desc(lse))]
-    stream = _ext.stream_of(q.device)
+    stream = _ext.stream_of(q.device) if stream is None else ctypes.c_void_p(stream.cuda_stream)
     if noalloc:
         rc = lib.dsv_tree_verify_noalloc(*args, inp.n_prefix, *tail, stream)
     else:
@@ -45,6 +45,26 @@ def test_noalloc_tree_verify_matches_workspace_entry_point(gpu, dsv_lib):
         o_w, l_w = _verify(dsv_lib, inp, par, noalloc=False)
         torch.cuda.synchronize()
         assert torch.equal(o_n, o_w) and torch.equal(l_n, l_w)
+
+
+def test_noalloc_calls_on_two_streams_are_serialised(gpu, dsv_lib):
+    """Two calls issued back to back on two streams, with no host
+    synchronisation between them, share the GPU's scratch array: the library
+    makes the second stream wait for the first call, so each result still
+    equals dsv_tree_verify's with its own workspace."""
+    cases = [(65536, 64, 1), (20000, 48, 2)]
+    inps = [wl.make_tree_verify_inputs(n_prefix=n, M=M, device=str(gpu), seed=s, tree_seed=M) for n, M, s in cases]
+    pars = [torch.tensor(i.parent, dtype=torch.int64, device=gpu) for i in inps]
+    want = [_verify(dsv_lib, i, p, noalloc=False) for i, p in zip(inps, pars)]
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(device=gpu), torch.cuda.Stream(device=gpu)
+    for rep in range(3):
+        print(f"[noalloc two streams] round {rep}", flush=True)
+        got = [_verify(dsv_lib, inps[0], pars[0], noalloc=True, stream=s1),
+               _verify(dsv_lib, inps[1], pars[1], noalloc=True, stream=s2)]
+        torch.cuda.synchronize()
+        for (o, l), (ow, lw) in zip(got, want):
+            assert torch.equal(o, ow) and torch.equal(l, lw)
 
 
 def test_noalloc_refuses_a_plan_beyond_its_scratch(gpu, dsv_lib):
