@@ -553,7 +553,7 @@ __device__ __forceinline__ double block_max_d(double v, double* scratch) {
 //   accept iff e^(y_tok - m) / z > min(eps, alpha e^-H)
 // with T, eps and alpha the arguments as given (float).  The whole workgroup
 // takes one flagged node at a time: two passes over the parent's row.
-__device__ __noinline__ void typical_recheck(const AcceptArgs& a, int t, const int* par, int* okv, const float* xtok) {
+__device__ __forceinline__ void typical_recheck(const AcceptArgs& a, int t, const int* par, int* okv, const float* xtok) {
   __shared__ double scratch[16];
   const double T = (double)a.temperature;
   const int64_t V = a.V;
@@ -736,7 +736,7 @@ __global__ void __launch_bounds__(1024) accept_walk_kernel(const AcceptArgs a) {
     tok_lds[i] = tok;
     int okc = okv[i];
     int node = i;
-    for (int h = 0; h < a.max_hops && okc; ++h) {
+    for (int h = 0; h < a.max_hops && okc && node != 0; ++h) {  // the root's parent is itself
       node = par[node];
       okc &= okv[node];
     }

@@ -371,3 +371,67 @@ def test_typical_decision_near_the_threshold(gpu, delta, sigma):
         info = run_and_compare(lg.to(gpu), draft.to(gpu), parent_ref.to(gpu), pos.to(gpu), 8, mode="typical", **kw)
         if dtype == torch.float32:
             assert (info[:, 1] == (1 if delta > 0 else 0)).all()
+
+
+def _accept_into(ws, logits, draft, parent_ref, pos, max_hops, mode, kw):
+    """dsv_tree_accept through the C ABI over a caller-owned workspace."""
+    from diffspec_mi355x import _ext
+    lib = _ext.load()
+    T, M, V = logits.shape
+    dev = logits.device
+    path = torch.empty((T, M), dtype=torch.int64, device=dev)
+    tokens = torch.empty_like(path)
+    info = torch.empty((T, 4), dtype=torch.int64, device=dev)
+    assert ws.numel() >= lib.dsv_accept_workspace_bytes(T, M, V)
+    mode_id = {"greedy": _ext.ACCEPT_GREEDY, "typical": _ext.ACCEPT_TYPICAL}[mode]
+    rc = lib.dsv_tree_accept(mode_id, _ext.desc(logits), _ext.desc(draft), _ext.desc(parent_ref), _ext.desc(pos),
+                             int(max_hops), float(kw.get("temperature", 1.0)),
+                             float(kw.get("posterior_threshold", 0.09)), float(kw.get("posterior_alpha", 0.3)),
+                             _ext.desc(path), _ext.desc(tokens), _ext.desc(info), _ext.desc(None), ws.data_ptr(),
+                             ws.numel(), _ext.stream_of(dev))
+    _ext.check(rc, "tree_accept")
+    return path.cpu().numpy(), tokens.cpu().numpy(), info.cpu().numpy()
+
+
+@pytest.mark.parametrize("mode", ["greedy", "typical"])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_acceptance_needs_no_cleared_workspace(gpu, mode, dtype):
+    """The result must not depend on what the workspace held before: zeros,
+    all ones, random bytes, the statistics of a call over other trees, and the
+    same workspace reused call after call.  bf16 rows take the streaming
+    sweep, f32 rows the generic one."""
+    kw = dict(temperature=1.0, posterior_threshold=0.09, posterior_alpha=0.3) if mode == "typical" else {}
+    T, M, V = 8, 64, 50000
+    a = wl.make_accept_inputs(T=T, M=M, V=V, dtype=dtype, device=str(gpu), seed=21, pos_offset=300)
+    other = wl.make_accept_inputs(T=T, M=M, V=V, dtype=dtype, device=str(gpu), seed=22, pos_offset=300)
+    lg = a.logits.float().cpu().numpy()
+    want = []
+    for t in range(T):
+        args = (lg[t], a.draft[t].cpu().numpy(), a.parent_ref[t].cpu().tolist(), a.pos[t].cpu().numpy(), 8)
+        if mode == "greedy":
+            want.append(oacc.greedy_walk(*args))
+        else:
+            want.append(oacc.typical_walk(*args, temperature=1.0, eps=0.09, alpha=0.3))
+
+    def check(res, label):
+        path, toks, info = res
+        for t, (w_toks, w_ids, w_alen, w_next, w_id) in enumerate(want):
+            L = len(w_ids)
+            assert info[t].tolist() == [w_id, w_alen, w_next, L], f"{label}: tree {t}"
+            assert path[t, :L].tolist() == w_ids and (path[t, L:] == -1).all(), f"{label}: tree {t}"
+            assert toks[t, :L].tolist() == w_toks and (toks[t, L:] == -1).all(), f"{label}: tree {t}"
+
+    from diffspec_mi355x import _ext
+    nbytes = _ext.load().dsv_accept_workspace_bytes(T, M, V)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=gpu)
+    g = torch.Generator(device=gpu).manual_seed(5)
+    run = lambda x: _accept_into(ws, x.logits, x.draft, x.parent_ref, x.pos, 10, mode, kw)
+    for label, fill in [("zeros", lambda: ws.zero_()), ("ones", lambda: ws.fill_(255)),
+                        ("random", lambda: ws.copy_(torch.randint(0, 256, (nbytes,), generator=g, device=gpu,
+                                                                  dtype=torch.uint8)))]:
+        fill()
+        check(run(a), label)
+    run(other)
+    check(run(a), "after a call over other trees")
+    for k in range(3):
+        check(run(a), f"reused {k}")
