@@ -141,7 +141,7 @@ int dsv_flash_attn_with_kvcache(const dsv_tensor* q, const dsv_tensor* k_cache,
  * tree_attention_forward — runtime/tree_attention.py:462-541 (mask handling of
  * _maybe_to_int8_mask, :449-460).
  *   q   [B, M, H, D];  k, v [B, M, Hk, D] (the post-cache tree block)
- *   tree_mask  [B, 1, T, T] or [B, T, T] with T >= M; the lower-right M x M
+ *   tree_mask  [B, 1, T, T] or [B, T, T] with T >= M (M <= 1024); the lower-right M x M
  *              block is used.  Float masks are additive (keep where == 0);
  *              int8 / uint8 / bool masks keep where != 0.
  *   prefix_lse [B, H, M] f32 (any layout reshaping to it, as the reference's
@@ -199,7 +199,8 @@ int dsv_verify_bundle_paged(const dsv_tensor* q, const dsv_tensor* kv_pages,
  *              tokens [n_prefix, n_prefix + M) of the same cache
  *              (KVCache.cat layout, runtime/cache_state.py:52-66)
  *   parent     [B, M] or [M] int32|int64: parent node of each tree node, < 0 for
- *              the root (the ancestor relation of runtime/draft_tree.py:188-214)
+ *              the root (the ancestor relation of runtime/draft_tree.py:188-214);
+ *              M <= 1024 nodes
  *   row_perm   optional [M] int32 node order used to pack query rows (bundle
  *              order, core/bundle_scheduler.py:42-123); ndim == 0 = identity.
  *              It must be a permutation of [0, M) (dsv_bundle_order's output

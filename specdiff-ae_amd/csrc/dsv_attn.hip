@@ -163,7 +163,9 @@ __device__ __forceinline__ float max16(const f32x16& s) {
 // MODE: kModeF32Paged / kModeF32Dense when both sources are known to use
 // 32-bit DMA offsets (the host checks), else kModeAny (per-source choice at
 // run time).
-template <typename T, int D, bool DMASK, int MODE>
+// BIG: trees of more than kTreeNodeM nodes (the tree split's visibility table
+// indexed by packed row instead of node).
+template <typename T, int D, bool DMASK, int MODE, bool BIG = false>
 __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
   using G = Geo<D>;
   constexpr int NW = 8;
@@ -177,7 +179,8 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
   static_assert(G::STAGES == 4, "the loop is unrolled over a 4-stage ring");
   constexpr int PT_OFF = G::RING;
   constexpr int VIS_OFF = PT_OFF + kPageLds * 4;
-  constexpr int LDS_BYTES = VIS_OFF + kTreeMaxM * kTreeMaxW * 8;
+  constexpr int VIS_W = BIG ? kTreeMaxW : kTreeNodeW;  // words per table entry
+  constexpr int LDS_BYTES = VIS_OFF + (BIG ? kTreeSlots : kTreeNodeM) * VIS_W * 8;
 
   // One LDS allocation so that the DMA ring sits at offset 0 (addresses < 64 KiB).
   __shared__ __attribute__((aligned(1024))) uint8_t smem[LDS_BYTES];
@@ -252,15 +255,25 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
         par_lds[i] = (int32_t)load_index(a.tpar, a.tpar_i64, b * a.tpar_sb + i * a.tpar_sm);
       __syncthreads();
     }
-    for (int i = tid; i < M; i += NT) {
-      uint64_t wd[kTreeMaxW];
+    // Entry e of the table: the ancestor-or-self bits of node e (up to
+    // kTreeNodeM nodes), or, with BIG, of the node of this workgroup's packed
+    // row e (0 <= e < 256, row = 256 * rb + e, node slot mi = row mod M).
+    const int n_ent = BIG ? min(kTreeSlots, a.R - rb * (NW * 32)) : M;
+    for (int e = tid; e < n_ent; e += NT) {
+      int i = e;
+      if constexpr (BIG) {
+        const int mi = (rb * (NW * 32) + e) % M;
+        // A permutation entry outside [0, M) is clamped, as for the Q rows.
+        i = a.row_perm ? min(max(a.row_perm[mi], 0), M - 1) : mi;
+      }
+      uint64_t wd[VIS_W];
 #pragma unroll
-      for (int x = 0; x < kTreeMaxW; ++x) wd[x] = 0;
+      for (int x = 0; x < VIS_W; ++x) wd[x] = 0;
       if (a.tpar != nullptr) {
         int node = i;
         for (int step = 0; step < M && node >= 0 && node < M; ++step) {
 #pragma unroll
-          for (int x = 0; x < kTreeMaxW; ++x)
+          for (int x = 0; x < VIS_W; ++x)
             if ((node >> 6) == x) wd[x] |= 1ull << (node & 63);
           const int p = par_lds[node];
           if (p == node) break;
@@ -270,13 +283,13 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
         for (int j = 0; j < M; ++j) {
           if (tmask_keep(a, b, i, j)) {
 #pragma unroll
-            for (int x = 0; x < kTreeMaxW; ++x)
+            for (int x = 0; x < VIS_W; ++x)
               if ((j >> 6) == x) wd[x] |= 1ull << (j & 63);
           }
         }
       }
 #pragma unroll
-      for (int x = 0; x < kTreeMaxW; ++x) vis_lds[i * kTreeMaxW + x] = wd[x];
+      for (int x = 0; x < VIS_W; ++x) vis_lds[e * VIS_W + x] = wd[x];
     }
   }
   __syncthreads();
@@ -472,7 +485,8 @@ __global__ void __launch_bounds__(512, 2) attn_splitk_kernel(const AttnArgs a) {
     }
     if (is_tree) {
       // Visibility bits of this tile's keys, shifted to this lane's keys.
-      const uint64_t vw = rvalid ? vis_lds[node_of * kTreeMaxW + (t >> 1)] : 0ull;
+      const int ent = BIG ? wid * 32 + lj : node_of;
+      const uint64_t vw = rvalid ? vis_lds[ent * VIS_W + (t >> 1)] : 0ull;
       const uint32_t vb = (uint32_t)(vw >> ((t & 1) * 32 + 4 * lg));
       keep &= (vb & 0xFu) | ((vb >> 4) & 0xF0u) | ((vb >> 8) & 0xF00u) | ((vb >> 12) & 0xF000u);
     }
@@ -737,10 +751,14 @@ hipError_t launch_t(const AttnArgs& a, hipStream_t s, hipEvent_t ev0, hipEvent_t
   const bool pp = a.pre.pt != nullptr, tp = a.has_tree ? a.tree.pt != nullptr : pp;
   const dim3 grid((unsigned)nblk), block(512);
   if constexpr (!DMASK) {
-    if (mp == kFast32 && mt == kFast32 && pp == tp) {
+    if (mp == kFast32 && mt == kFast32 && pp == tp && !(a.has_tree && a.M > kTreeNodeM)) {
       if (pp) return launch_k(attn_splitk_kernel<T, D, DMASK, kModeF32Paged>, grid, block, s, ev0, ev1, a);
       return launch_k(attn_splitk_kernel<T, D, DMASK, kModeF32Dense>, grid, block, s, ev0, ev1, a);
     }
+  }
+  if constexpr (!DMASK) {
+    if (a.has_tree && a.M > kTreeNodeM)
+      return launch_k(attn_splitk_kernel<T, D, DMASK, kModeAny, true>, grid, block, s, ev0, ev1, a);
   }
   return launch_k(attn_splitk_kernel<T, D, DMASK, kModeAny>, grid, block, s, ev0, ev1, a);
 }

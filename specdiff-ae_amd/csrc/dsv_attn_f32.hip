@@ -87,7 +87,7 @@ __global__ void __launch_bounds__(512, 1) attn_f32_kernel(const AttnArgs a) {
   constexpr int K_OFF = 0, V_OFF = K_OFF + KT * KROW * 4;
   constexpr int PT_OFF = V_OFF + D * VROW * 4;
   constexpr int VIS_OFF = PT_OFF + kPageLds * 4;
-  constexpr int LDS_BYTES = VIS_OFF + kTreeMaxM * kTreeMaxW * 8;
+  constexpr int LDS_BYTES = VIS_OFF + kTreeSlots * kTreeMaxW * 8;
   __shared__ __attribute__((aligned(16))) uint8_t smem[LDS_BYTES];
   float* ks = reinterpret_cast<float*>(smem + K_OFF);
   float* vts = reinterpret_cast<float*>(smem + V_OFF);
@@ -146,7 +146,17 @@ __global__ void __launch_bounds__(512, 1) attn_f32_kernel(const AttnArgs a) {
         par_lds[i] = (int32_t)load_index(a.tpar, a.tpar_i64, b * a.tpar_sb + i * a.tpar_sm);
       __syncthreads();
     }
-    for (int i = tid; i < M; i += NT) {
+    // Entry lr of the table: the ancestor-or-self bits (kTreeMaxW words, of
+    // which the first ceil(M/64) are used) of the node of this block's packed
+    // row lr (0 <= lr < 256, row = 256 * rb + lr, node slot mi = row mod M).
+    const int W = (M + 63) >> 6;
+    const int row_first = rb * (NW * 32);
+    for (int lr = tid; lr < kTreeSlots; lr += NT) {
+      const int row = row_first + lr;
+      if (row >= a.R) break;
+      const int mi = row % M;
+      // A permutation entry outside [0, M) is clamped, as for the Q rows.
+      const int i = a.row_perm ? min(max(a.row_perm[mi], 0), M - 1) : mi;
       uint64_t wd[kTreeMaxW];
 #pragma unroll
       for (int x = 0; x < kTreeMaxW; ++x) wd[x] = 0;
@@ -170,7 +180,8 @@ __global__ void __launch_bounds__(512, 1) attn_f32_kernel(const AttnArgs a) {
         }
       }
 #pragma unroll
-      for (int x = 0; x < kTreeMaxW; ++x) vis_lds[i * kTreeMaxW + x] = wd[x];
+      for (int x = 0; x < kTreeMaxW; ++x)
+        if (x < W) vis_lds[lr * kTreeMaxW + x] = wd[x];
     }
   }
   __syncthreads();
@@ -264,7 +275,7 @@ __global__ void __launch_bounds__(512, 1) attn_f32_kernel(const AttnArgs a) {
         keep |= (uint32_t)(kb + key < ke) << v;
       }
       if (is_tree) {
-        const uint64_t vw = rvalid ? vis_lds[node_of * kTreeMaxW + (t >> 1)] : 0ull;
+        const uint64_t vw = rvalid ? vis_lds[(wid * 32 + lj) * kTreeMaxW + (t >> 1)] : 0ull;
         const uint32_t vb = (uint32_t)(vw >> ((t & 1) * 32 + 4 * lg));
         keep &= (vb & 0xFu) | ((vb >> 4) & 0xF0u) | ((vb >> 8) & 0xF00u) | ((vb >> 12) & 0xF000u);
       }

@@ -24,8 +24,15 @@ struct F16 {};
 
 // Limits of the in-kernel tables (checked by the host before launch).
 constexpr int kPageLds = 1040;       // page-table entries staged per split
-constexpr int kTreeMaxM = 256;       // tree nodes handled by the tree split
-constexpr int kTreeMaxW = kTreeMaxM / 64;
+constexpr int kTreeMaxM = 1024;      // tree nodes handled by the tree split
+constexpr int kTreeMaxW = kTreeMaxM / 64;  // 64-bit visibility words per node
+// The tree split's visibility table: up to kTreeNodeM nodes it is indexed by
+// node (kTreeNodeW words each); larger trees take a table indexed by the
+// workgroup's 256 packed rows (query head g, node slot mi: row = g * M + mi),
+// kTreeMaxW words each.
+constexpr int kTreeNodeM = 256;
+constexpr int kTreeNodeW = kTreeNodeM / 64;
+constexpr int kTreeSlots = 256;
 
 // A key/value source: contiguous [B, N, Hk, D] or a page pool half
 // [P, Hk, page, D] addressed through a page table.

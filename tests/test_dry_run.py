@@ -135,7 +135,10 @@ def pool_half(pool, layer, kv):
     # several 256-row blocks per KV head over many splits
     (6000, 256, 16, 32, 8, 128, False), (30000, 192, 16, 32, 8, 128, False),
     # the second workload of tests/test_gpu_graphs.py
-    (1000, 20, 16, 32, 8, 128, False)])
+    (1000, 20, 16, 32, 8, 128, False),
+    # trees beyond 256 nodes (tests/test_gpu_attention.py::test_tree_verify_trees_beyond_256_nodes)
+    (2000, 300, 16, 8, 2, 128, False), (500, 512, 16, 8, 2, 128, True), (100, 1024, 16, 8, 2, 128, True),
+    (300, 1024, 16, 8, 2, 128, False), (1000, 700, 4, 8, 2, 64, False), (64, 257, 16, 32, 8, 128, True)])
 def test_tree_verify_paged_and_dense(dry, n_prefix, M, ps, H, Hk, D, perm):
     a = Alloc()
     B = 1
@@ -163,7 +166,8 @@ def test_tree_verify_paged_and_dense(dry, n_prefix, M, ps, H, Hk, D, perm):
 @pytest.mark.parametrize("n_prefix,M,ps,H,Hk,D,perm", [
     (4096, 64, 16, 32, 8, 128, False), (0, 64, 16, 32, 8, 128, False), (100, 7, 16, 32, 8, 128, True),
     (1000, 64, 1, 8, 2, 128, False), (1000, 64, 4, 8, 2, 64, False), (1000, 64, 64, 8, 2, 128, True),
-    (6000, 256, 16, 32, 8, 128, False), (30000, 192, 16, 32, 8, 128, False)])
+    (6000, 256, 16, 32, 8, 128, False), (30000, 192, 16, 32, 8, 128, False),
+    (1000, 400, 16, 8, 2, 128, True), (200, 1024, 16, 8, 2, 64, False)])
 def test_tree_verify_paged_and_dense_f32(dry, n_prefix, M, ps, H, Hk, D, perm):
     """The fp32 kernel's loads, over the shapes the fp32 GPU tests launch."""
     a = Alloc()
@@ -239,6 +243,20 @@ def test_inconsistent_shapes_are_rejected_before_any_access(dry):
     rc = dry.dsv_prefix_attention_forward(ctypes.byref(q), ctypes.byref(k_short), ctypes.byref(v), -1,
                                           ctypes.byref(out), ctypes.byref(lse), wsp, ws, None)
     assert rc == -1 and "shapes differ" in _ext.last_error()
+
+
+def test_tree_verify_refuses_trees_beyond_1024_nodes(dry):
+    a = Alloc()
+    B, M, H, Hk, D, N = 1, 1025, 8, 2, 128, 100
+    q = tensor(a, (B, M, H, D))
+    kc, vc = tensor(a, (B, N + M, Hk, D)), tensor(a, (B, N + M, Hk, D))
+    par = tensor(a, (M,), _ext.DSV_I64)
+    out, lse = tensor(a, (B, M, H, D)), tensor(a, (B, M, H), _ext.DSV_F32)
+    ws = 1 << 30
+    rc = dry.dsv_tree_verify(ctypes.byref(q), ctypes.byref(kc), ctypes.byref(vc), ctypes.byref(none()), N,
+                             ctypes.byref(par), ctypes.byref(none()), ctypes.byref(out), ctypes.byref(lse),
+                             a.take(256), ws, None)
+    assert rc == -2 and "1024" in _ext.last_error()
 
 
 @pytest.mark.parametrize("ps", [16, 4])

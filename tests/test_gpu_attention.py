@@ -333,6 +333,58 @@ def test_tree_verify_dense_equals_paged_and_perm_invariant(gpu):
     assert torch.equal(o_p, o_b) and torch.equal(l_p, l_b)
 
 
+@pytest.mark.parametrize("n_prefix,M,shape,dtype,ps", [
+    (2000, 300, "random", torch.bfloat16, 16), (500, 512, "random", torch.bfloat16, 16),
+    (100, 1024, "random", torch.bfloat16, 16), (300, 1024, "chain", torch.bfloat16, 16),
+    (1000, 700, "star", torch.float16, 4), (1000, 400, "random", torch.float32, 16),
+    (64, 257, "random", torch.bfloat16, 16)])
+def test_tree_verify_trees_beyond_256_nodes(gpu, n_prefix, M, shape, dtype, ps):
+    """Trees of 257 to 1024 nodes.  A workgroup of the tree split owns 256
+    packed query rows, whose nodes' ancestor masks it holds in one LDS table
+    per block: against the fp64 oracle (chain, star and generated trees;
+    bf16, f16 and f32), and the bundle row order bit-equal to the identity
+    order."""
+    print(f"[tree_verify large tree] n_prefix={n_prefix} M={M} shape={shape} dtype={dtype} ps={ps}", flush=True)
+    inp = wl.make_tree_verify_inputs(n_prefix=n_prefix, M=M, H=8, Hk=2, D=128, page_size=ps, dtype=dtype,
+                                     scale=1.0, seed=M, tree_seed=M + 1, max_depth=12, max_outdeg=6,
+                                     device=str(gpu))
+    if shape == "chain":
+        inp.parent = [-1] + list(range(M - 1))
+    elif shape == "star":
+        inp.parent = [-1] + [0] * (M - 1)
+    par = torch.tensor(inp.parent, dtype=torch.int64, device=gpu)
+    out, lse = tree_verify(inp.q, inp.kv_pages[0, 0], inp.kv_pages[0, 1], n_prefix, par, page_table=inp.page_table,
+                           out_dtype=torch.float32)
+    perm = torch.tensor(bundle_row_order(inp.parent, num_bundles=8), dtype=torch.int32, device=gpu)
+    o_b, l_b = tree_verify(inp.q, inp.kv_pages[0, 0], inp.kv_pages[0, 1], n_prefix, par, page_table=inp.page_table,
+                           row_perm=perm, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(out, o_b) and torch.equal(lse, l_b)
+    o_ref, l_ref = oracle_tree_verify(inp)
+    assert_attn_close(np64(out[0]), o_ref, rel=4e-3)
+    assert_lse_close(np64(lse[0]), l_ref)
+
+
+def test_tree_attention_forward_300_nodes(gpu):
+    """The tree block alone with a dense [B, 1, T, T] mask over 300 nodes (the
+    mask read per node slot of each 256-row block)."""
+    B, M, H, Hk, D, T = 1, 300, 8, 2, 128, 310
+    q = rand((B, M, H, D), 17, torch.bfloat16, gpu)
+    k = rand((B, M, Hk, D), 18, torch.bfloat16, gpu)
+    v = rand((B, M, Hk, D), 19, torch.bfloat16, gpu)
+    keep = oa.ancestor_mask(wl.make_tree(M, seed=6, max_depth=12, max_outdeg=6)[0])
+    full = np.zeros((B, 1, T, T), dtype=bool)
+    full[:, 0, -M:, -M:] = keep
+    mask = torch.from_numpy(full).to(torch.int8).to(gpu)
+    plse = (torch.randn(B, H, M) * 2 + 8).to(gpu)
+    cur, w, lse_t = tree_attention_forward(q, k, v, mask, 0, plse, B, M, H, D, return_lse=True)
+    torch.cuda.synchronize()
+    o_ref, w_ref, l_ref = oa.tree_attention(np64(q[0]), np64(k[0]), np64(v[0]), keep, np64(plse[0]))
+    assert_attn_close(np64(cur[0]), o_ref)
+    assert_lse_close(np64(lse_t[0]), l_ref)
+    np.testing.assert_allclose(np64(w[0])[..., 0], w_ref, atol=8e-3)
+
+
 @pytest.mark.parametrize("shape", ["chain", "star"])
 def test_tree_verify_special_trees(gpu, shape):
     M, n_prefix = 32, 200
