@@ -355,6 +355,9 @@ size_t dsv_lmhead_accept_workspace_bytes(int64_t T, int64_t M, int64_t V);
  *               dsv_tree_accept
  *   logits_out  optional bf16 [T, M, V]: also write the logits (ndim 0 to skip)
  * The weight is streamed once per 64 hidden rows (T * M <= 64: once).
+ * Typical mode decides near-threshold nodes again in float64 from the
+ * written logits, as dsv_tree_accept does; without logits_out it keeps the
+ * decision of the fp32 statistics.
  */
 int dsv_lmhead_accept(int mode, const dsv_tensor* hidden, const dsv_tensor* weight,
                       const dsv_tensor* draft, const dsv_tensor* parent,

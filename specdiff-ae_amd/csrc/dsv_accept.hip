@@ -697,7 +697,8 @@ __global__ void __launch_bounds__(1024) accept_walk_kernel(const AcceptArgs a) {
   // typical test is decided from the sweep's fp32 statistics unless the
   // draft token's probability lies within the margin typical_margin() of the
   // threshold: such nodes (okv = 2) are decided again from float64
-  // statistics of the parent's row, below.
+  // statistics of the parent's row, below (with the fused lm_head, only when
+  // it writes the logits: a.logits is null otherwise).
   bool recheck = false;
   if (i < M) {
     int ok = 1;
@@ -711,7 +712,7 @@ __global__ void __launch_bounds__(1024) accept_walk_kernel(const AcceptArgs a) {
           const float prob = __builtin_amdgcn_exp2f(fmaf(xtok, a.inv_temp * kLog2e, -mz[p])) / lz[p];
           const float thr = fminf(a.eps, a.alpha * __expf(-hz[p]));
           ok = prob > thr;
-          recheck = a.xtok == nullptr && a.logits != nullptr && prob == prob && thr == thr &&
+          recheck = a.logits != nullptr && prob == prob && thr == thr &&
                     fabsf(prob - thr) <= typical_margin(mz[p]) * thr;
         }
       }

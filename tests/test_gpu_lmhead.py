@@ -116,3 +116,41 @@ def test_strided_hidden_temperature_and_shared_positions(gpu):
     torch.cuda.synchronize()
     for k in ("next", "info", "path", "tokens"):
         assert torch.equal(r[k], ref[k]), k
+
+
+@pytest.mark.parametrize("delta", [1e-6, -1e-6])
+def test_typical_near_the_threshold_rechecked_from_the_written_logits(gpu, delta):
+    """With its logits written, the fused path re-decides near-threshold nodes
+    from them exactly as kernel 4 does.  Hidden rows that are unit vectors
+    make every logit an exact copy of one weight column, so rows within a
+    relative 1e-6 of the typical threshold (then rounded to bf16, many
+    inside the fp32 margin) can be planted as the roots' distributions."""
+    from oracle import accept as oacc
+    from test_gpu_accept import _near_threshold_rows
+    V, Dm, temperature = 20000, 64, 0.9
+    rng = np.random.default_rng(77 + (delta > 0))
+    rows, _ = _near_threshold_rows(24, V, delta, 0.5, rng, temperature=temperature)
+    T = min(rows.shape[0], Dm // 2)
+    rows16 = torch.from_numpy(rows[:T]).to(torch.bfloat16)
+    r16 = np.array([np.divide(*oacc.typical_prob_thr(rows16[t].double().numpy(), 0, temperature, 0.09, 0.3))
+                    for t in range(T)])
+    assert (np.abs(r16 - 1) < 5e-3).sum() >= T // 3, r16     # inside the margin: re-checked
+    w = torch.zeros((V, Dm), dtype=torch.bfloat16)
+    h = torch.zeros((T, 2, Dm), dtype=torch.bfloat16)
+    for t in range(T):
+        w[:, 2 * t] = rows16[t]
+        h[t, 0, 2 * t] = 1.0                                    # the root's logits: row t
+        h[t, 1, 2 * t + 1] = 1.0                                # the child's: zeros
+    draft = torch.zeros((T, 2), dtype=torch.int64)               # the child drafts token 0
+    pref = torch.full((T, 1), -1, dtype=torch.int64)
+    pos = torch.tensor([0, 1])
+    r = lmhead_tree_accept(h.to(gpu), w.to(gpu), draft.to(gpu), pref.to(gpu), pos.to(gpu), 2, mode="typical",
+                           temperature=temperature, posterior_threshold=0.09, posterior_alpha=0.3,
+                           return_logits=True)
+    lg = r["logits"].float().cpu().numpy()
+    assert np.array_equal(lg[:, 0], rows16.float().numpy())
+    info = r["info"].cpu().numpy()
+    for t in range(T):
+        w_toks, w_ids, w_alen, w_next, w_id = oacc.typical_walk(lg[t], draft[t].numpy(), [-1], pos.numpy(), 8,
+                                                                 temperature=temperature, eps=0.09, alpha=0.3)
+        assert info[t].tolist() == [w_id, w_alen, w_next, len(w_ids)], f"tree {t}"
