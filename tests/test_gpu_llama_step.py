@@ -65,6 +65,11 @@ def test_llama8b_shaped_verify_step(gpu):
     step = np.exp2(np.floor(np.log2(np.abs(top2[:, 1]))) - 7)  # one bf16 step at the top logit
     near_tie = (top2[:, 1] - top2[:, 0]) <= 2 * step
     assert np.all((nf == nt) | near_tie), np.nonzero((nf != nt) & ~near_tie)
+    # How often the exemption is used: the fused logits and torch's GEMM round
+    # their fp32 sums in different orders, so only near ties may differ.
+    n_tie, n_diff = int(near_tie.sum()), int((nf != nt).sum())
+    print(f"[llama step] near ties {n_tie} of {len(nf)} nodes, next tokens differing {n_diff}", flush=True)
+    assert n_diff <= max(1, len(nf) // 16), (n_tie, n_diff)
     if np.array_equal(nf, nt):
         assert torch.equal(rf["info"], r["info"]) and torch.equal(rf["path"], r["path"])
     print(f"[llama step] accept_length {w_alen}, next-token agreement {np.mean(nf == nt):.3f}", flush=True)
