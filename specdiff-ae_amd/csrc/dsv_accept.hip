@@ -95,14 +95,24 @@ __global__ void __launch_bounds__(kRowThreads) accept_rowstat_kernel(const Accep
   const bool aligned = ((reinterpret_cast<uintptr_t>(base + lo) & 15) == 0);
   if (aligned) {
     const int64_t nvec = (hi - lo) / VEC;
-    for (int64_t vi = threadIdx.x; vi < nvec; vi += kRowThreads) {
-      const u32x4 raw = *reinterpret_cast<const u32x4*>(base + lo + vi * VEC);
+    auto consume_vec = [&](const u32x4& raw, int64_t vi) {
       float xs[VEC];
       const LT* el = reinterpret_cast<const LT*>(&raw);
 #pragma unroll
       for (int e = 0; e < VEC; ++e) xs[e] = to_f<LT>(el[e]);
       consume(xs, VEC, lo + vi * VEC);
+    };
+    // Four of the thread's vectors in flight at a time, consumed in the
+    // same (increasing) order as one at a time.
+    int64_t vi = threadIdx.x;
+    for (; vi + 3 * kRowThreads < nvec; vi += 4 * kRowThreads) {
+      u32x4 raw[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) raw[u] = *reinterpret_cast<const u32x4*>(base + lo + (vi + u * kRowThreads) * VEC);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) consume_vec(raw[u], vi + u * kRowThreads);
     }
+    for (; vi < nvec; vi += kRowThreads) consume_vec(*reinterpret_cast<const u32x4*>(base + lo + vi * VEC), vi);
     for (int64_t k = lo + nvec * VEC + threadIdx.x; k < hi; k += kRowThreads) {
       const float x = to_f<LT>(base[k]);
       consume(&x, 1, k);
