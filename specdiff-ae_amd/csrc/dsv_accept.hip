@@ -419,19 +419,24 @@ __global__ void __launch_bounds__(kStrThreads) accept_stream16_kernel(const Acce
   int f = 0x7fffffff;
   if (!has_nan && bk == kstar && bs >= 0) {
     // This thread holds the maximum: its first index, from the sub-tile where
-    // the thread's maximum first occurred (re-read; rare).
+    // the thread's maximum first occurred, re-read with all of the thread's
+    // vectors of it in flight at once (one round trip instead of one per
+    // vector).
     if (bs == nsub) {
       f = 8 * nvec + tid;
     } else {
-      for (int v = 0; v < kStrVec && f == 0x7fffffff; ++v) {
+      u32x4 rr[kStrVec];
+#pragma unroll
+      for (int v = 0; v < kStrVec; ++v)
+        rr[v] = reinterpret_cast<const u32x4*>(rb)[min(bs * kSubVec + tid + kStrThreads * v, nvec - 1)];
+#pragma unroll
+      for (int v = 0; v < kStrVec; ++v) {
         const int vi = bs * kSubVec + tid + kStrThreads * v;
-        if (vi >= nvec) break;
-        const u32x4 r = reinterpret_cast<const u32x4*>(rb)[vi];
+#pragma unroll
         for (int w = 0; w < 8; ++w)
-          if ((key2((r[w >> 1] >> (16 * (w & 1))) & 0xFFFFu) & 0xFFFFu) == kstar) {
+          if (f == 0x7fffffff && vi < nvec &&
+              (key2((rr[v][w >> 1] >> (16 * (w & 1))) & 0xFFFFu) & 0xFFFFu) == kstar)
             f = 8 * vi + w;
-            break;
-          }
       }
     }
   }
