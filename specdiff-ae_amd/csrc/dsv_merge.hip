@@ -55,12 +55,15 @@ __global__ void __launch_bounds__(256) lse_merge_kernel(const MergeArgs a) {
   // (exactly so for 8 KV heads and batch 1).
   const int nb = gridDim.x;
   const int bx = ((nb & 7) == 0) ? (blockIdx.x & 7) * (nb >> 3) + (blockIdx.x >> 3) : blockIdx.x;
-  const int64_t row = (int64_t)bx * 4 + (threadIdx.x >> 6);
+  // The row index is uniform over the wave and below 2^31 (the host checks):
+  // its decomposition is 32-bit scalar arithmetic.
+  const int row = __builtin_amdgcn_readfirstlane(bx * 4 + (threadIdx.x >> 6));
   const int64_t nrows = (int64_t)a.B * a.Hk * a.R;
   if (row >= nrows) return;
-  const int r = (int)(row % a.R);
-  const int kvh = (int)((row / a.R) % a.Hk);
-  const int b = (int)(row / ((int64_t)a.R * a.Hk));
+  const int q = row / a.R;
+  const int r = row - q * a.R;
+  const int b = q / a.Hk;
+  const int kvh = q - b * a.Hk;
 
   float mrun = kNegInf;  // running maximum (log2 units), uniform over the wave
   float lsum = 0.f;      // this lane's share of sum_s w_s (per split group)
@@ -154,6 +157,7 @@ __global__ void __launch_bounds__(256) lse_merge_kernel(const MergeArgs a) {
 hipError_t launch_merge(const MergeArgs& a, hipStream_t s) {
   const int64_t nrows = (int64_t)a.B * a.Hk * a.R;
   if (nrows <= 0) return hipSuccess;
+  if (nrows >= ((int64_t)1 << 31) - 4) return hipErrorInvalidValue;
   const dim3 grid((unsigned)((nrows + 3) / 4));
   if (a.D == 128)
     hipLaunchKernelGGL((lse_merge_kernel<128, 8>), grid, dim3(256), 0, s, a);
