@@ -161,6 +161,30 @@ def bench_verify(args, lib, ev):
     return inp, total_ms / args.steps, k1_ms, t_wall, se0.elapsed_time(se1) / args.steps
 
 
+def bench_prefix_sweep(args, lib, ev):
+    """The metric's step (64 nodes, H 32, Hk 8, D 128, paged bf16) over prefix
+    lengths from 4K to 512K tokens, with enough KV layers rotated that the
+    layers together exceed the 256 MB Infinity Cache: us per step, kernel 1
+    (launch-attached events) and its algorithmic HBM rate."""
+    import types
+    rows = []
+    for n in (4096, 16384, 65536, 262144, 524288):
+        per_layer = 2 * n * 8 * 128 * 2
+        layers = max(1, min(24, -(-320 * 2 ** 20 // per_layer)))
+        sub = types.SimpleNamespace(**vars(args))
+        sub.n_prefix, sub.layers, sub.settle_ms = n, layers, 30.0
+        print(f"[bench] prefix sweep: N={n} layers={layers}", file=sys.stderr, flush=True)
+        inp, ms_step, k1_ms, _, _ = bench_verify(sub, lib, ev)
+        del inp
+        torch.cuda.empty_cache()
+        nb = algorithmic_bytes(n, args.nodes, 32, 8, 128)["kernel1"]
+        k1 = statistics.mean(k1_ms) * 1e3
+        rows.append({"n_prefix": n, "kv_layers_rotated": layers, "us_per_step": round(ms_step * 1e3, 2),
+                     "kernel1_us": round(k1, 2), "kernel1_hbm_gbs": round(nb / (k1 * 1e-6) / 1e9, 1),
+                     "kernel1_hbm_frac": round(nb / (k1 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+    return rows
+
+
 def bench_bundle_packed_128k(args, lib, ev):
     """128K paged prefix, 128-node tree (depth <= 12, out-degree <= 6), query
     rows packed in bundle order (8 bundles).  MFMA-bound: 512 flop/B.  A step
@@ -605,6 +629,8 @@ def main():
     ap.add_argument("--no-accept", action="store_true")
     ap.add_argument("--no-bundle-128k", action="store_true")
     ap.add_argument("--no-llama-step", action="store_true")
+    ap.add_argument("--prefix-sweep", action="store_true",
+                    help="also measure the step at prefix lengths 4K to 512K (prefix_sweep)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy (scale reference for the FETCH_SIZE / WRITE_SIZE "
                          "counters) and exit")
@@ -668,6 +694,8 @@ def main():
                                "second pass of K steps", "us_per_step_in_that_pass": round(ms_step_ev * 1e3, 3)},
         "wall_s_timed": round(t_wall, 4),
     }
+    if args.prefix_sweep:
+        line["prefix_sweep"] = bench_prefix_sweep(args, lib, ev)
     if not args.no_bundle_128k:
         print("[bench] bundle-packed verify (N=131072, M=128)", file=sys.stderr, flush=True)
         line["bundle_packed_128k"] = bench_bundle_packed_128k(args, lib, ev)
