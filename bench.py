@@ -41,6 +41,23 @@ import torch  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, AMD public spec
 
+# Untimed continuous load before every timed measurement (set by --settle-ms).
+# After an idle gap the GPU first runs at a boost clock for about 2 ms, then
+# 25-50 % slower for 10-20 ms while its power management settles, then at the
+# steady state a serving loop sees; each measurement starts in the last.
+SETTLE_MS = 60.0
+
+
+def settle(fn, ms=None, batch=10):
+    """Runs fn untimed, `batch` calls between synchronisations, for about
+    `ms` milliseconds (SETTLE_MS by default)."""
+    ms = SETTLE_MS if ms is None else ms
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(batch):
+            fn()
+        torch.cuda.synchronize()
+
 
 def algorithmic_bytes(n_prefix, M, H, Hk, D, elem=2, out_elem=2, page_size=16):
     kv = 2 * n_prefix * Hk * D * elem
@@ -120,15 +137,10 @@ def bench_verify(args, lib, ev):
         k, v = pools[i % len(pools)]
         return tree_verify(inp.q, k, v, n_prefix, par, page_table=inp.page_table)
 
-    # Settle: after idle the GPU runs this step ~20-30% slower for the first
-    # ~30 ms of continuous load while its clocks ramp to the steady state a
-    # serving loop sees.  Untimed steps run for args.settle_ms first; then the
-    # W warm-up steps, then the K timed ones.
-    t_settle = time.perf_counter()
-    while (time.perf_counter() - t_settle) * 1e3 < args.settle_ms:
-        for i in range(20):
-            step(i)
-        torch.cuda.synchronize()
+    # Settle (untimed steps for args.settle_ms), then the W warm-up steps,
+    # then the K timed ones.
+    it = iter(range(1 << 62))
+    settle(lambda: step(next(it)), args.settle_ms, batch=20)
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
@@ -172,7 +184,7 @@ def bench_prefix_sweep(args, lib, ev):
         per_layer = 2 * n * 8 * 128 * 2
         layers = max(1, min(24, -(-320 * 2 ** 20 // per_layer)))
         sub = types.SimpleNamespace(**vars(args))
-        sub.n_prefix, sub.layers, sub.settle_ms = n, layers, 30.0
+        sub.n_prefix, sub.layers = n, layers
         print(f"[bench] prefix sweep: N={n} layers={layers}", file=sys.stderr, flush=True)
         inp, ms_step, k1_ms, _, _ = bench_verify(sub, lib, ev)
         del inp
@@ -211,6 +223,8 @@ def bench_bundle_packed_128k(args, lib, ev):
         return tree_verify(inp.q, k, v, N, par, page_table=inp.page_table, row_perm=perm, check_row_perm=False)
 
     n = 20
+    it = iter(range(1 << 62))
+    settle(lambda: step(next(it)), args.settle_ms, batch=5)
     for i in range(10):
         step(i)
     torch.cuda.synchronize()
@@ -261,8 +275,8 @@ def bench_bundle_packed_128k(args, lib, ev):
 
 def device_us(fn, calls=10, reps=20):
     """Device time per call of fn: `calls` calls captured once in a HIP graph,
-    replayed `reps` times (host launch cost excluded).  fn records no memset
-    nodes."""
+    replayed `reps` times (host launch cost excluded) after the graph has been
+    replayed untimed for SETTLE_MS.  fn records no memset nodes."""
     for _ in range(3):
         fn()
     torch.cuda.synchronize()
@@ -272,6 +286,7 @@ def device_us(fn, calls=10, reps=20):
             fn()
     g.replay()
     torch.cuda.synchronize()
+    settle(g.replay, batch=1)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(reps):
@@ -302,6 +317,7 @@ def bench_llama8b_step(args, lib, ev):
     for _ in range(3):
         r = st.step()
     torch.cuda.synchronize()
+    settle(st.step, batch=1)
     n = 10
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
@@ -502,6 +518,7 @@ def bench_accept(args, lib, ev):
         for _ in range(3):
             tree_accept(a.logits, a.draft, a.parent_ref, a.pos, 10, mode=mode, **kw)
         torch.cuda.synchronize()
+        settle(lambda: tree_accept(a.logits, a.draft, a.parent_ref, a.pos, 10, mode=mode, **kw))
         n = 20
         evs = ev.create(2 * n)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -635,6 +652,8 @@ def main():
                     help="only run a 1 GiB device-to-device copy (scale reference for the FETCH_SIZE / WRITE_SIZE "
                          "counters) and exit")
     args = ap.parse_args()
+    global SETTLE_MS
+    SETTLE_MS = args.settle_ms
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (got --gpus {args.gpus}). "
               "Run with --gpus 1.", file=sys.stderr)
