@@ -646,8 +646,8 @@ def main():
     ap.add_argument("--no-accept", action="store_true")
     ap.add_argument("--no-bundle-128k", action="store_true")
     ap.add_argument("--no-llama-step", action="store_true")
-    ap.add_argument("--prefix-sweep", action="store_true",
-                    help="also measure the step at prefix lengths 4K to 512K (prefix_sweep)")
+    ap.add_argument("--no-prefix-sweep", action="store_true",
+                    help="skip the step at prefix lengths 4K to 512K (prefix_sweep)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device-to-device copy (scale reference for the FETCH_SIZE / WRITE_SIZE "
                          "counters) and exit")
@@ -713,7 +713,7 @@ def main():
                                "second pass of K steps", "us_per_step_in_that_pass": round(ms_step_ev * 1e3, 3)},
         "wall_s_timed": round(t_wall, 4),
     }
-    if args.prefix_sweep:
+    if not args.no_prefix_sweep:
         line["prefix_sweep"] = bench_prefix_sweep(args, lib, ev)
     if not args.no_bundle_128k:
         print("[bench] bundle-packed verify (N=131072, M=128)", file=sys.stderr, flush=True)

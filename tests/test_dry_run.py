@@ -123,7 +123,7 @@ def pool_half(pool, layer, kv):
 @pytest.mark.parametrize("n_prefix,M,ps,H,Hk,D,perm", [
     (4096, 64, 16, 32, 8, 128, False), (0, 64, 16, 32, 8, 128, False), (100, 7, 16, 32, 8, 128, False),
     (1000, 128, 16, 32, 8, 128, True), (16, 256, 16, 32, 8, 128, False), (65536, 64, 16, 32, 8, 128, False),
-    # the prefix lengths of bench.py --prefix-sweep
+    # the prefix lengths of bench.py's prefix sweep
     (4096, 64, 16, 32, 8, 128, False), (16384, 64, 16, 32, 8, 128, False), (262144, 64, 16, 32, 8, 128, False),
     (524288, 64, 16, 32, 8, 128, False),
     (131072, 128, 16, 32, 8, 128, True), (3000, 64, 16, 32, 8, 128, True), (200, 32, 16, 32, 8, 128, False),
