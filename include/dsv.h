@@ -96,7 +96,10 @@ int64_t dsv_dry_run_checks(void);
 /*
  * Workspace needed by any attention entry point for queries of shape
  * [B, M, H, D] against keys with Hk heads and n_keys prefix keys, with an
- * optional tree block (has_tree != 0).  Returns 0 on invalid arguments.
+ * optional tree block (has_tree != 0).  Returns 0 on invalid arguments and
+ * on sizes beyond the kernels' 32-bit counts (batch <= 2^20, query heads <=
+ * 65536, keys <= 2^40, H / Hk * M <= 2^24, B * H * M <= 2^30), which every
+ * attention entry point refuses with DSV_ERR_UNSUPPORTED.
  */
 size_t dsv_attn_workspace_bytes(int64_t B, int64_t M, int64_t H, int64_t Hk,
                                 int64_t D, int64_t n_keys, int64_t page_size,
@@ -105,7 +108,7 @@ size_t dsv_attn_workspace_bytes(int64_t B, int64_t M, int64_t H, int64_t Hk,
 /*
  * prefix_attention_forward — runtime/tree_attention.py:414-446; LSE layout of
  * flash_attn_with_kvcache(return_softmax_lse=True), runtime/attention_compat.py:103-132.
- *   q   [B, M, H, D] bf16|f16
+ *   q   [B, M, H, D] bf16|f16|f32 (f32 inputs are computed in fp32)
  *   k,v [B, N, Hk, D] same dtype; H % Hk == 0 (Hk == H is the repeat_kv'd form)
  *   n_keys  keys [0, n_keys) are attended (cache_seqlens); n_keys < 0 means N
  *   out [B, M, H, D] q dtype or f32;  lse [B, H, M] f32 (natural log)
@@ -121,7 +124,7 @@ int dsv_prefix_attention_forward(const dsv_tensor* q, const dsv_tensor* k,
  * flash-attn contract it stands in for: keys [0, cache_seqlens[b]) of batch
  * b, causal masking aligned to the end of that range, softmax_lse
  * [B, H, M]).
- *   q              [B, M, H, D] bf16|f16;  k_cache, v_cache [B, N, Hk, D]
+ *   q              [B, M, H, D] bf16|f16|f32;  k_cache, v_cache [B, N, Hk, D]
  *   cache_seqlens  optional [B] int32|int64 per-batch length (clamped to
  *                  [0, n_keys]); ndim 0 = every batch uses n_keys
  *   n_keys         scalar length (the reference's int cache_seqlens); < 0 = N
@@ -390,7 +393,9 @@ int dsv_lmhead_accept(int mode, const dsv_tensor* hidden, const dsv_tensor* weig
  *   page_table  [n_logical] int32|int64
  *   start       cache length before the tree (first tree token)
  *   q, q_out    optional [M, H, D] or [1, M, H, D] (ndim 0 to skip)
- * D must be a multiple of 16; token rows 16-byte aligned.
+ * D must be a multiple of 16; token rows 16-byte aligned.  Sizes: M <= 2^24,
+ * Hk and H <= 65536, D <= 4096, and (2 * Hk + H) * M * D / 16 <= 2^31
+ * (DSV_ERR_UNSUPPORTED beyond).
  * Aliasing: inputs (k, v, q, cos, sin) may not overlap outputs (k_dst, v_dst,
  * q_out), nor outputs each other (DSV_ERR_INVALID), except row for row in
  * place: q_out == q with the same strides, or, with a dense cache, k (v)

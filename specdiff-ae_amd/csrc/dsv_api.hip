@@ -136,6 +136,7 @@ struct Plan {
   int G = 0, R = 0, n_rb = 0, n_splits = 0, s_total = 0;
   int64_t kps = 0;
   size_t opart_bytes = 0, ml_bytes = 0, total = 0;
+  const char* err = nullptr;  // sizes beyond the kernels' 32-bit counts (nothing planned)
 };
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
@@ -146,8 +147,16 @@ Plan make_plan(int64_t B, int64_t M, int64_t H, int64_t Hk, int64_t D, int64_t n
                bool has_tree) {
   Plan p;
   const int rows_per_block = dsv::attn_rows_per_block();
+  // Row, split and workgroup counts are 32-bit in the kernels and the merge.
+  const bool in_range = B <= (1 << 20) && M <= (1 << 24) && H <= (1 << 16) && n_keys <= ((int64_t)1 << 40);
+  const int64_t R = in_range ? (H / Hk) * M : 0;
+  if (!in_range || R > ((int64_t)1 << 24) || B * Hk * R > ((int64_t)1 << 30)) {
+    p.err = "sizes beyond the attention kernels' range (batch <= 2^20, heads <= 65536, keys <= 2^40, query heads / "
+            "key heads x rows <= 2^24, batch x query heads x rows <= 2^30)";
+    return p;
+  }
   p.G = (int)(H / Hk);
-  p.R = (int)(p.G * M);
+  p.R = (int)R;
   p.n_rb = (int)((p.R + rows_per_block - 1) / rows_per_block);
   const int64_t units = B * Hk * p.n_rb;
   if (n_keys > 0) {
@@ -161,7 +170,13 @@ Plan make_plan(int64_t B, int64_t M, int64_t H, int64_t Hk, int64_t D, int64_t n
     int64_t kps = ((n_keys + s0 - 1) / s0 + 31) / 32 * 32;
     kps = std::min(std::max<int64_t>(kps, 32), kps_max);
     p.kps = kps;
-    p.n_splits = (int)((n_keys + kps - 1) / kps);
+    const int64_t ns = (n_keys + kps - 1) / kps;
+    if (units * (ns + 1) >= ((int64_t)1 << 31)) {
+      p = Plan{};
+      p.err = "the key splits need more than 2^31 workgroups";
+      return p;
+    }
+    p.n_splits = (int)ns;
   }
   p.s_total = p.n_splits + (has_tree ? 1 : 0);
   const size_t rows = (size_t)p.s_total * B * Hk * p.R;
@@ -231,6 +246,7 @@ KvSrc dense_src(const dsv_tensor* k, const dsv_tensor* v, int64_t key0) {
 }
 
 int check_ws(const Plan& p, void* ws, size_t ws_bytes) {
+  if (p.err != nullptr) return fail(DSV_ERR_UNSUPPORTED, "%s", p.err);
   if (p.total == 0) return DSV_OK;
   if (ws == nullptr || ws_bytes < p.total)
     return fail(DSV_ERR_WORKSPACE, "workspace of %zu bytes required (got %zu)", p.total, ws_bytes);
@@ -878,6 +894,10 @@ int dsv_kv_append(const dsv_tensor* k, const dsv_tensor* v, const dsv_tensor* co
   if (vs[0] != M || vs[1] != Hk || vs[2] != D) return fail(DSV_ERR_INVALID, "v must match k");
   if (M < 1 || Hk < 1) return fail(DSV_ERR_INVALID, "empty k");
   if (D % 16 != 0) return fail(DSV_ERR_UNSUPPORTED, "head_dim %lld must be a multiple of 16", (long long)D);
+  // The kernel's counts are 32-bit and its grid covers one thread per
+  // 16-element chunk of every row.
+  if (M > (1 << 24) || Hk > (1 << 16) || D > (1 << 12))
+    return fail(DSV_ERR_UNSUPPORTED, "k is too large (M <= 2^24, key heads <= 65536, head_dim <= 4096)");
   if (start < 0) return fail(DSV_ERR_INVALID, "start must be >= 0");
 
   dsv::AppendArgs a{};
@@ -918,6 +938,7 @@ int dsv_kv_append(const dsv_tensor* k, const dsv_tensor* v, const dsv_tensor* co
     if (q->dtype != k->dtype || q_out->dtype != k->dtype) return fail(DSV_ERR_INVALID, "q and q_out must have the dtype of k");
     if (qs[0] != M || qs[2] != D || os[0] != M || os[1] != qs[1] || os[2] != D)
       return fail(DSV_ERR_INVALID, "q and q_out must be [M, H, D]");
+    if (qs[1] > (1 << 16)) return fail(DSV_ERR_UNSUPPORTED, "q has more than 65536 heads");
     a.H = (int)qs[1];
     a.q = static_cast<const uint16_t*>(q->data);
     a.q_sm = qst[0];
@@ -926,6 +947,8 @@ int dsv_kv_append(const dsv_tensor* k, const dsv_tensor* v, const dsv_tensor* co
     a.qo_sm = ost[0];
     a.qo_sh = ost[1];
   }
+  if ((2 * M * Hk + (int64_t)a.H * M) * (D / 16) > ((int64_t)1 << 31))
+    return fail(DSV_ERR_UNSUPPORTED, "k, v and q hold more than 2^31 16-element chunks");
   for (dsv_tensor* t : {k_dst, v_dst}) {
     const char* nm = t == k_dst ? "k_dst" : "v_dst";
     if (t == nullptr || t->data == nullptr) return fail(DSV_ERR_INVALID, "%s missing", nm);

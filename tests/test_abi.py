@@ -118,6 +118,20 @@ def test_validation_errors_are_reported(dsv_lib):
     assert rc == -3 and "workspace" in _ext.last_error()
 
 
+def test_attention_refuses_sizes_beyond_its_32_bit_counts(dsv_lib):
+    # Query rows per KV head above 2^24, and batch x heads x rows above 2^30:
+    # refused with a message, and no workspace is planned for them.
+    for B, M in ((1, 1 << 23), (1 << 10, 1 << 20)):
+        q = _t((B, M, 32, 128))
+        k = _t((B, 64, 8, 128))
+        lse = _t((B, 32, M), _ext.DSV_F32)
+        rc = dsv_lib.dsv_prefix_attention_forward(ctypes.byref(q), ctypes.byref(k), ctypes.byref(k), -1,
+                                                  ctypes.byref(q), ctypes.byref(lse), None, 0, None)
+        assert rc == -2 and "range" in _ext.last_error()
+        assert dsv_lib.dsv_attn_workspace_bytes(B, M, 32, 8, 128, 64, 0, 0) == 0
+    assert dsv_lib.dsv_attn_workspace_bytes(1, 64, 32, 8, 128, 65536, 16, 1) > 0
+
+
 def test_accept_validation(dsv_lib):
     logits = _t((2, 8, 100), _ext.DSV_BF16)
     draft = _t((2, 8), _ext.DSV_I64)
@@ -239,6 +253,23 @@ def test_kv_append_validation(dsv_lib):
     finally:
         dsv_lib.dsv_set_dry_run(0)
     assert rc == 0
+
+
+def test_kv_append_refuses_sizes_beyond_its_32_bit_counts(dsv_lib):
+    # The descriptors are never dereferenced: the sizes are refused first.
+    none = _ext.DsvTensor()
+    k = _t(((1 << 24) + 1, 1, 16))
+    dst = _t((1, (1 << 24) + 8, 16))
+    rc = dsv_lib.dsv_kv_append(ctypes.byref(k), ctypes.byref(k), ctypes.byref(none), ctypes.byref(none),
+                               ctypes.byref(dst), ctypes.byref(dst), ctypes.byref(none), 0, ctypes.byref(none),
+                               ctypes.byref(none), None)
+    assert rc == -2 and "too large" in _ext.last_error()
+    k = _t((1 << 20, 1 << 10, 64))  # 2^31 chunks of k and v
+    dst = _t((1 << 10, (1 << 20) + 8, 64))
+    rc = dsv_lib.dsv_kv_append(ctypes.byref(k), ctypes.byref(k), ctypes.byref(none), ctypes.byref(none),
+                               ctypes.byref(dst), ctypes.byref(dst), ctypes.byref(none), 0, ctypes.byref(none),
+                               ctypes.byref(none), None)
+    assert rc == -2 and "2^31" in _ext.last_error()
 
 
 def test_kv_append_rejects_aliasing_except_row_for_row_in_place(dsv_lib):
