@@ -71,6 +71,30 @@ def test_accept_fp32_64_nodes_vocab128256_seed1(gpu, mode):
         assert info[0, 1] == max(depth)
 
 
+def test_accept_random_shapes_bit_exact(gpu):
+    """40 random acceptance calls against the oracle walk: 1-4 trees of 1 to
+    1024 nodes, vocabularies of 3 to 50257, bf16 / f16 / f32 logits of spread
+    0.3 to 3 (planted paths), greedy and typical (temperature 0.5 to 1.7)."""
+    rng = np.random.default_rng(5)
+    for case in range(40):
+        T = int(rng.integers(1, 5))
+        M = int(rng.choice([1, 2, 9, 64, 100, 256, 300, 1024]))
+        V = int(rng.choice([3, 100, 1000, 32000, 50257]))
+        dtype = [torch.bfloat16, torch.float16, torch.float32][int(rng.integers(3))]
+        mode = "greedy" if rng.integers(2) == 0 else "typical"
+        sigma = float(rng.choice([0.3, 1.0, 3.0]))
+        depth = int(rng.integers(1, 13))
+        while sum(6 ** k for k in range(depth + 1)) < M:
+            depth += 1
+        temp = float(rng.choice([0.5, 1.0, 1.7]))
+        print(f"[accept random] case {case}: T={T} M={M} V={V} {dtype} {mode} sigma={sigma} depth={depth} "
+              f"temperature={temp}", flush=True)
+        a = wl.make_accept_inputs(T=T, M=M, V=V, dtype=dtype, sigma=sigma, seed=300 + case, max_depth=depth,
+                                  max_outdeg=6, pos_offset=int(rng.integers(0, 100000)), device=str(gpu))
+        kw = dict(temperature=temp, posterior_threshold=0.09, posterior_alpha=0.3) if mode == "typical" else {}
+        run_and_compare(a.logits, a.draft, a.parent_ref, a.pos, depth, mode=mode, **kw)
+
+
 def test_typical_accepts_runner_up_that_greedy_rejects(gpu):
     V, M = 5000, 6
     lg = torch.full((1, M, V), -4.0)

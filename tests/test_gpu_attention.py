@@ -319,6 +319,92 @@ def test_tree_verify_random_configurations(gpu):
         assert_lse_close(np64(l_p[0]), l_ref, what=f"case {case}")
 
 
+def test_tree_verify_wide_random_sweep(gpu):
+    """60 random configurations over a wider range than the test above: prefix
+    lengths at tile and page boundaries (0 .. 17000), trees of 1 to 600 nodes
+    (the >256-node instantiation included), seven GQA groupings, head_dim 64
+    and 128, pages of 1 to 64 tokens, bf16 / f16 / f32, with and without
+    bundle packing.  Paged and dense results against the fp64 oracle; bit-equal
+    to each other whenever both plan the same splits (with pages of a few
+    tokens a long split is capped at the page-table slice staged in LDS, so
+    the paged plan can hold more, shorter splits and round differently)."""
+    from diffspec_mi355x import _ext
+    lib = _ext.load()
+    rng = np.random.default_rng(2026)
+    for case in range(60):
+        n_prefix = int(rng.choice([0, 1, 2, 31, 32, 33, 63, 64, 65, 500, 1000, 4095, 4097, 9000, 17000]))
+        M = int(rng.choice([1, 2, 3, 17, 32, 33, 64, 65, 128, 200, 255, 256, 257, 300, 511, 600]))
+        H, Hk = [(8, 8), (32, 8), (16, 4), (8, 2), (4, 1), (12, 4), (2, 2)][int(rng.integers(7))]
+        D = int(rng.choice([64, 128]))
+        ps = int(rng.choice([1, 2, 4, 16, 32, 64]))
+        dtype = [torch.bfloat16, torch.float16, torch.float32][int(rng.integers(3))]
+        depth, outdeg = int(rng.integers(1, 13)), int(rng.integers(1, 7))
+        while sum(outdeg ** k for k in range(depth + 1)) < M:
+            depth, outdeg = depth + 1, min(outdeg + 1, 6)
+        perm_on, nb = bool(rng.integers(2)), int(rng.integers(1, 9))
+        what = f"case {case}: N={n_prefix} M={M} H={H}/{Hk} D={D} ps={ps} {dtype} depth={depth} perm={perm_on}"
+        print(f"[tree_verify wide] {what}", flush=True)
+        inp = wl.make_tree_verify_inputs(n_prefix=n_prefix, M=M, H=H, Hk=Hk, D=D, page_size=ps, dtype=dtype,
+                                         seed=1000 + case, tree_seed=2000 + case, max_depth=depth,
+                                         max_outdeg=outdeg, device=str(gpu))
+        par = torch.tensor(inp.parent, dtype=torch.int64, device=gpu)
+        perm = None
+        if perm_on:
+            perm = torch.tensor(bundle_row_order(inp.parent, num_bundles=nb), dtype=torch.int32, device=gpu)
+        o_p, l_p = tree_verify(inp.q, inp.kv_pages[0, 0], inp.kv_pages[0, 1], n_prefix, par,
+                               page_table=inp.page_table, row_perm=perm)
+        o_d, l_d = tree_verify(inp.q, inp.logical_kv(0, 0).contiguous(), inp.logical_kv(0, 1).contiguous(), n_prefix,
+                               par, row_perm=perm)
+        torch.cuda.synchronize()
+        if (lib.dsv_attn_workspace_bytes(1, M, H, Hk, D, n_prefix, ps, 1)
+                == lib.dsv_attn_workspace_bytes(1, M, H, Hk, D, n_prefix, 0, 1)):
+            assert torch.equal(o_p, o_d) and torch.equal(l_p, l_d), f"{what}: paged differs from dense"
+        o_ref, l_ref = oracle_tree_verify(inp)
+        rel = 4e-3 if dtype == torch.float32 else 1e-2
+        for o_, l_, kind in ((o_p, l_p, "paged"), (o_d, l_d, "dense")):
+            assert_attn_close(np64(o_[0]), o_ref, rel=rel, what=f"{what} {kind}")
+            assert_lse_close(np64(l_[0]), l_ref, what=f"{what} {kind}")
+
+
+def test_flash_attn_random_causal_and_lengths(gpu):
+    """30 random flash_attn_with_kvcache calls: batch 1-3 with a random length
+    per batch (0 .. N), causal or not, bf16 / f16 / f32, against the fp64
+    oracle; rows that see no key are zero with LSE -inf."""
+    from diffspec_mi355x.runtime.attention_compat import flash_attn_with_kvcache
+    rng = np.random.default_rng(77)
+    for case in range(30):
+        B = int(rng.integers(1, 4))
+        N = int(rng.choice([1, 33, 200, 1000, 5000]))
+        M = int(rng.choice([1, 5, 16, 48, 64, 100]))
+        H, Hk = [(8, 8), (32, 8), (16, 4), (4, 1)][int(rng.integers(4))]
+        D = int(rng.choice([64, 128]))
+        dtype = [torch.bfloat16, torch.float16, torch.float32][int(rng.integers(3))]
+        causal = bool(rng.integers(2))
+        lens = rng.integers(0, N + 1, size=B)
+        what = f"case {case}: B={B} N={N} M={M} H={H}/{Hk} D={D} {dtype} causal={causal} lens={lens.tolist()}"
+        print(f"[flash_attn random] {what}", flush=True)
+        q = rand((B, M, H, D), 10 + case, dtype, gpu)
+        k = rand((B, N, Hk, D), 20 + case, dtype, gpu)
+        v = rand((B, N, Hk, D), 30 + case, dtype, gpu)
+        sl = torch.tensor(lens, dtype=torch.int32, device=gpu)
+        out, lse = flash_attn_with_kvcache(q, k, v, cache_seqlens=sl, causal=causal, return_softmax_lse=True)
+        torch.cuda.synchronize()
+        for b in range(B):
+            n = int(lens[b])
+            keep = np.ones((M, n), dtype=bool)
+            if causal:
+                for m in range(M):
+                    keep[m, max(0, n - M + m + 1):] = False
+            o_ref, l_ref = oa.masked_attention(np64(q[b]), np64(k[b, :n]), np64(v[b, :n]), keep)
+            got_o, got_l = np64(out[b]), np64(lse[b])
+            vis = keep.any(axis=1)
+            if vis.any():
+                assert_attn_close(got_o[vis], o_ref[vis], rel=4e-3 if dtype == torch.float32 else 1e-2,
+                                  what=f"{what} b={b}")
+            assert (got_o[~vis] == 0).all(), f"{what} b={b}: rows without keys are not zero"
+            assert_lse_close(got_l.T, l_ref, what=f"{what} b={b}")
+
+
 def test_tree_verify_dense_equals_paged_and_perm_invariant(gpu):
     inp = paged_case(gpu, 3000, 64, tree_seed=5)
     par = torch.tensor(inp.parent, dtype=torch.int32, device=gpu)
