@@ -78,6 +78,32 @@ def test_fused_matches_kernel4_on_its_logits(gpu, T, M, Dm, V, mode):
         assert int(r["info"][:, 1].max()) >= 1   # the planted paths are (at least partly) accepted
 
 
+def test_fused_random_shapes(gpu):
+    """20 random fused lm_head calls: 1-3 trees of 1 to 100 nodes, hidden
+    sizes 64 to 1024, vocabularies of 1 to 20000 (around the 256-row slices),
+    greedy and typical; the written logits within one bf16 step of fp64, the
+    walk and next tokens bit-exact against kernel 4 on those logits."""
+    rng = np.random.default_rng(92)
+    for case in range(20):
+        T = int(rng.integers(1, 4))
+        M = int(rng.choice([1, 2, 7, 33, 64, 100]))
+        Dm = int(rng.choice([64, 128, 192, 256, 320, 512, 1024]))
+        V = int(rng.choice([1, 2, 255, 256, 257, 1000, 5000, 20000]))
+        mode = "greedy" if rng.integers(2) == 0 else "typical"
+        print(f"[lmhead random] case {case}: T={T} M={M} Dm={Dm} V={V} {mode}", flush=True)
+        h, w, draft, pref, pos, md = _case(gpu, T, M, Dm, V, seed=900 + case)
+        hops = min(md + 2, M)
+        r = lmhead_tree_accept(h, w, draft, pref, pos, hops, mode=mode, return_next=True, return_logits=True)
+        torch.cuda.synchronize()
+        lg = r["logits"]
+        _check_logits(h.reshape(T * M, Dm), w, lg.reshape(T * M, V))
+        ref = tree_accept(lg, draft, pref, pos, hops, mode=mode, return_next=True)
+        torch.cuda.synchronize()
+        assert torch.equal(r["next"], ref["next"]) and torch.equal(r["next"], lg.argmax(-1))
+        assert torch.equal(r["info"], ref["info"])
+        assert torch.equal(r["path"], ref["path"]) and torch.equal(r["tokens"], ref["tokens"])
+
+
 def test_without_logits_output_and_llama_shape(gpu):
     # Llama-3.1-8B lm_head: Dm 4096, V 128256; 64 nodes.  The logits are
     # checked on a vocabulary subset against the fp64 oracle.

@@ -45,6 +45,32 @@ def test_sample_walk_bit_exact(gpu, dtype, temperature, top_p, top_k):
     run_and_compare(a.logits, a.draft, a.parent_ref, a.pos, 8, temperature, top_p, top_k, seed=12345)
 
 
+def test_sample_random_warper_combinations(gpu):
+    """30 random sampling calls, bit-exact against the oracle: 1-3 trees of 1
+    to 200 nodes, vocabularies of 2 to 32000, bf16 / f16 / f32 logits of
+    spread 0.1 to 8, temperature 0.3 to 1.5, top-p 1 down to 0.001, top-k 0
+    to 1000, random 64-bit seeds."""
+    rng = np.random.default_rng(91)
+    for case in range(30):
+        T = int(rng.integers(1, 4))
+        V = int(rng.choice([2, 7, 1000, 5003, 32000]))
+        M = int(rng.choice([1, 5, 64, 200]))
+        dtype = [torch.bfloat16, torch.float16, torch.float32][int(rng.integers(3))]
+        temp = float(rng.choice([0.3, 0.7, 1.0, 1.5]))
+        top_p = float(rng.choice([1.0, 0.95, 0.5, 0.05, 0.001]))
+        top_k = int(rng.choice([0, 1, 5, 50, 1000]))
+        sigma = float(rng.choice([0.1, 1.0, 3.0, 8.0]))
+        depth = int(rng.integers(1, 10))
+        while sum(6 ** k for k in range(depth + 1)) < M:
+            depth += 1
+        seed = int(rng.integers(0, 2 ** 63))
+        print(f"[sample random] case {case}: T={T} M={M} V={V} {dtype} temperature={temp} top_p={top_p} "
+              f"top_k={top_k} sigma={sigma}", flush=True)
+        a = wl.make_accept_inputs(T=T, M=M, V=V, dtype=dtype, sigma=sigma, seed=500 + case, max_depth=depth,
+                                  max_outdeg=6, device=str(gpu))
+        run_and_compare(a.logits, a.draft, a.parent_ref, a.pos, depth, temp, top_p, top_k, seed)
+
+
 def test_sample_full_vocab_64_nodes(gpu):
     """bf16 [1, 64, 128256] N(0, 3) logits, temperature 0.7, top-p 0.9, top-k 50."""
     a = wl.make_accept_inputs(T=1, M=64, V=128256, device=str(gpu), seed=21)
