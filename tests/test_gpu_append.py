@@ -86,3 +86,56 @@ def test_append_without_rope_is_a_copy(gpu):
     assert torch.equal(kc[:, start:start + M], k.permute(1, 0, 2))
     assert torch.equal(vc[:, start:start + M], v.permute(1, 0, 2))
     assert int((kc[:, :start] != 0).sum()) == 0 and int((kc[:, start + M:] != 0).sum()) == 0
+
+
+def test_append_random_shapes(gpu):
+    """20 random appends, bit-exact against torch's op sequence: 1 to 300 tree
+    tokens, 1-8 key heads, 1-32 query heads (with or without q), head_dim 16
+    to 256, bf16 / f16, with or without RoPE, into dense caches or page pools
+    of 1- to 64-token pages behind a random permutation."""
+    rng = np.random.default_rng(45)
+    for case in range(20):
+        dtype = [torch.bfloat16, torch.float16][int(rng.integers(2))]
+        M, Hk = int(rng.choice([1, 3, 64, 300])), int(rng.choice([1, 2, 8]))
+        D = int(rng.choice([16, 64, 128, 256]))
+        H = Hk * int(rng.choice([1, 4])) if rng.integers(2) else 0
+        rope, paged = bool(rng.integers(2)), bool(rng.integers(2))
+        start = int(rng.integers(0, 200))
+        print(f"[append random] case {case}: {dtype} M={M} Hk={Hk} H={H} D={D} rope={rope} paged={paged} "
+              f"start={start}", flush=True)
+        g = torch.Generator().manual_seed(case)
+        k = (torch.randn((M, Hk, D), generator=g) * 2).to(dtype).to(gpu)
+        v = torch.randn((M, Hk, D), generator=g).to(dtype).to(gpu)
+        q = (torch.randn((M, H, D), generator=g) * 2).to(dtype).to(gpu) if H else None
+        cos, sin = _tables(M, D, dtype, start + 1000, gpu) if rope else (None, None)
+        if paged:
+            ps = int(rng.choice([1, 2, 16, 64]))
+            n_pages = (start + M + ps - 1) // ps
+            kp = torch.randn((n_pages + 2, Hk, ps, D), generator=g).to(dtype).to(gpu)
+            vp = torch.randn((n_pages + 2, Hk, ps, D), generator=g).to(dtype).to(gpu)
+            pt = torch.from_numpy(rng.permutation(n_pages + 2)[:n_pages].astype(np.int32)).to(gpu)
+            tok = torch.arange(start + M, device=gpu)
+            phys, slot = pt[tok // ps].long(), tok % ps
+            k0, v0 = kp[phys, :, slot].clone(), vp[phys, :, slot].clone()      # logical view [n, Hk, D]
+            q_out = append_tree_kv(k, v, kp, vp, start, cos=cos, sin=sin, page_table=pt, q=q)
+            kl, vl = kp[phys, :, slot], vp[phys, :, slot]
+        else:
+            S = start + M + int(rng.integers(0, 9))
+            kc = torch.randn((Hk, S, D), generator=g).to(dtype).to(gpu)
+            vc = torch.randn((Hk, S, D), generator=g).to(dtype).to(gpu)
+            k0, v0 = kc.permute(1, 0, 2).clone(), vc.permute(1, 0, 2).clone()
+            q_out = append_tree_kv(k, v, kc, vc, start, cos=cos, sin=sin, q=q)
+            kl, vl = kc.permute(1, 0, 2), vc.permute(1, 0, 2)
+        torch.cuda.synchronize()
+        if rope:
+            kt = k.permute(1, 0, 2)
+            want_k = ((kt * cos) + (_rotate_half(kt, D) * sin)).permute(1, 0, 2)
+        else:
+            want_k = k
+        assert torch.equal(kl[start:start + M], want_k), f"case {case} k"
+        assert torch.equal(vl[start:start + M], v), f"case {case} v"
+        assert torch.equal(kl[:start], k0[:start]) and torch.equal(vl[:start], v0[:start]), f"case {case} prefix"
+        if H:
+            qt = q.permute(1, 0, 2)
+            want_q = ((qt * cos) + (_rotate_half(qt, D) * sin)).permute(1, 0, 2) if rope else q
+            assert torch.equal(q_out.reshape(M, H, D), want_q), f"case {case} q"

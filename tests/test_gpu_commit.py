@@ -101,3 +101,45 @@ def test_out_of_range_path_entries_stay_inside_the_tree_slots(gpu):
     got = x.float().cpu().numpy()
     want = oacc.kv_commit(cache.float().numpy(), start, [0, 7, 0, 3])
     assert np.array_equal(got, want)
+
+
+def test_commit_random_layouts(gpu):
+    """24 random commits, bit-exact: dense caches of 1-4 leading dimensions
+    (layers, K/V, batch, heads) in bf16 / f16 / f32 with head_dim 8 to 256,
+    and page pools of 1- to 64-token pages behind a random permutation; paths
+    are random root-first increasing node lists of 1 to M nodes."""
+    rng = np.random.default_rng(44)
+    for case in range(24):
+        dtype = [torch.bfloat16, torch.float16, torch.float32][int(rng.integers(3))]
+        esize = 4 if dtype == torch.float32 else 2
+        D = int(rng.choice([d for d in (8, 16, 64, 128, 256) if (d * esize) % 16 == 0]))
+        M = int(rng.choice([1, 5, 24, 64, 128]))
+        M = min(M, 65536 // (D * esize))                  # the kernel's row budget: M * row bytes <= 64 KiB
+        n = int(rng.integers(1, M + 1))
+        path = [0] + sorted(rng.choice(np.arange(1, M), size=n - 1, replace=False).tolist()) if M > 1 else [0]
+        paged = bool(rng.integers(2))
+        print(f"[commit random] case {case}: {dtype} D={D} M={M} path={len(path)} paged={paged}", flush=True)
+        p, info = _path_info(path, M, gpu)
+        if not paged:
+            start = int(rng.integers(0, 100))
+            lead = tuple(int(x) for x in rng.integers(1, 4, size=int(rng.integers(1, 5))))
+            cache = torch.randn(lead + (start + M + int(rng.integers(0, 9)), D)).to(dtype)
+            want = oacc.kv_commit(cache.float().numpy(), start, path)
+            x = cache.to(gpu)
+            kv_commit(x, start, p, info)
+            torch.cuda.synchronize()
+            assert np.array_equal(x.float().cpu().numpy(), want), f"case {case}"
+        else:
+            ps = int(rng.choice([1, 2, 16, 64]))
+            start = int(rng.integers(0, 300))
+            L, Hk = int(rng.integers(1, 3)), int(rng.integers(1, 4))
+            n_pages = (start + M + ps - 1) // ps
+            pool = torch.randn((L, 2, n_pages + 3, Hk, ps, D)).to(dtype).to(gpu)
+            pt = torch.from_numpy(rng.permutation(n_pages + 3)[:n_pages].astype(np.int32)).to(gpu)
+            tok = torch.arange(start + M, device=gpu)
+            # the logical view: tokens first ([n, L, 2, Hk, D]), then on axis -2 for the oracle
+            before = np.moveaxis(pool[:, :, pt[tok // ps].long(), :, tok % ps].float().cpu().numpy(), 0, -2)
+            kv_commit(pool, start, p, info, page_table=pt)
+            torch.cuda.synchronize()
+            got = np.moveaxis(pool[:, :, pt[tok // ps].long(), :, tok % ps].float().cpu().numpy(), 0, -2)
+            assert np.array_equal(got, oacc.kv_commit(before, start, path)), f"case {case}"
