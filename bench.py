@@ -581,8 +581,9 @@ def cpu_baseline(inp, args):
     from oracle import ref_cpu_path as rc
     from oracle import attention as oa
 
-    # Every core of the affinity mask, unless the box caps this process's CPU
-    # share through OMP_NUM_THREADS (the GPU boxes give one GPU 16 threads).
+    # Every core of the affinity mask, unless the machine caps this process's
+    # CPU share through OMP_NUM_THREADS (a shared host may give each GPU's
+    # process a fixed number of threads).
     affinity = len(os.sched_getaffinity(0))
     cores = min(affinity, int(os.environ.get("OMP_NUM_THREADS", affinity)))
     torch.set_num_threads(cores)
